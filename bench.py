@@ -1,0 +1,247 @@
+"""Benchmark of the decode hot path on one MI355X.
+
+Default workload: the 36-layer decode sweep at the Qwen3-4B GQA shape at
+10240 tokens — every layer its own K/V cache [1, 8, 10240, 128] fp16 (1.5 GB
+in total, past the 256 MB Infinity Cache) and its own query [1, 32, 1, 128].
+One step is one decode token through the model's attention: 36 sequential
+calls, each the split-KV partial kernel plus the LSE combine kernel, replayed
+as one HIP graph. Inputs are resident in HBM before the timed region.
+
+Printed JSON line:
+- value: algorithmic GB/s of the whole step (K+V read, Q read, O written:
+  10240*4096 + 16384 bytes per call), us_per_call next to it;
+- roofline: the partial kernel alone, algorithmic bytes per launch over its
+  mean duration from HIP events around a graph of 36 partial launches;
+- cpu_baseline: the reference's CPU decode path (torch SDPA with the query
+  heads folded, fp16, threadcut/attention.py:40-42) on the host cores;
+- splice: the 36-layer suffix splice (Split(2048, 8668, 5668), 14336-token
+  caches, theta 1e6) in one launch, algorithmic GB/s (C of K and V read and
+  written).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "flash-decode µs/call & HBM GB/s (% of peak), Qwen3-4B GQA shape, 10k ctx"
+PEAK_GBS = 8000.0
+LAYERS, HQ, HKV, D = 36, 32, 8, 128
+
+
+def decode_bytes(n, batch=1):
+    return batch * (2 * HKV * n * D * 2 + 2 * HQ * D * 2)
+
+
+def splice_bytes(c, layers=LAYERS):
+    return 4 * layers * HKV * c * D * 2
+
+
+def read_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/<name>), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def time_graph(graph, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per replay
+
+
+def capture(fn):
+    import torch
+
+    fn()  # eager warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def cpu_baseline(n, seconds):
+    """The reference's CPU decode path on one call of the workload, bounded to ~`seconds`."""
+    import torch
+
+    from oracle.decode import folded_sdpa
+    from threadcut_amd import workloads
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    q, k, v, _ = workloads.decode_inputs(2, n=n)
+    scale = D ** -0.5
+    for _ in range(3):
+        folded_sdpa(q, k, v, scale)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        folded_sdpa(q, k, v, scale)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    return {"value": round(decode_bytes(n) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} single decode calls (q [1,32,1,128], K/V [1,8,{n},128] fp16) of the "
+                      f"reference's CPU path (torch SDPA, query heads folded), median {t * 1e6:.1f} us/call",
+            "us_per_call": round(t * 1e6, 2)}
+
+
+def bench_splice(dev, steps, warmup):
+    import torch
+
+    from threadcut_amd import _lib, kv, workloads
+
+    s = workloads.SPLICE_SPLIT
+    n = workloads.SPLICE_TOKENS
+    ks, vs = workloads.layer_caches(1, LAYERS, n, device=dev)
+    table = _lib.float_array(kv.rope_table(-s.gap, workloads.inv_freq(1e6)))
+    lib = _lib.load()
+    kp = _lib.ptr_array([t.data_ptr() for t in ks])
+    vp = _lib.ptr_array([t.data_ptr() for t in vs])
+    st = _lib.i64x3(*ks[0].stride()[:3])
+
+    def run():
+        # The same move every time: the buffers' contents change, the work does not.
+        _lib.check(lib.tc_splice_rope(kp, vp, LAYERS, st, 1, HKV, n, D, _lib.TC_DTYPE_F16, s.a, s.c0, s.c,
+                                      table, _lib.stream_of(dev)), "tc_splice_rope")
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gbs = splice_bytes(s.c) / (ms * 1e-3) / 1e9
+    return {"us_per_splice": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+            "bytes": splice_bytes(s.c), "config": {"layers": LAYERS, "tokens": n, "split": [s.a, s.c0, s.c],
+                                                   "theta": 1e6}}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--n", type=int, default=10240, help="KV tokens per layer")
+    ap.add_argument("--split", type=int, default=0, help="tokens per KV split (0: tuned)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-splice", action="store_true")
+    ap.add_argument("--only", choices=["decode", "partial", "splice"], default=None,
+                    help="run one measurement only (for profiling)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the decode path is measured on a single MI355X "
+              f"(got --gpus {args.gpus}, WORLD_SIZE {world}); multi-GPU sharding is not part of this build.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from threadcut_amd import flash_decode, workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.only == "splice":
+        print(json.dumps(bench_splice(dev, args.steps, args.warmup)))
+        return
+
+    n = args.n
+    scale = D ** -0.5
+    ks, vs = workloads.layer_caches(2, LAYERS, n, device=dev)
+    gq = torch.Generator(device=dev)
+    gq.manual_seed(2)
+    qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+    plans = [flash_decode.DecodePlan(q, k, v, scale, o, split=args.split or None)
+             for q, k, v, o in zip(qs, ks, vs, outs)]
+
+    def step():
+        for p in plans:
+            p.run()
+
+    def step_partial():
+        for p in plans:
+            p.run_partial()
+
+    result = {}
+    if args.only in (None, "decode"):
+        g = capture(step)
+        ms = time_graph(g, args.steps, args.warmup)
+        result["ms"] = ms
+    if args.only in (None, "partial"):
+        gp = capture(step_partial)
+        ms_p = time_graph(gp, args.steps, args.warmup)
+        result["ms_partial"] = ms_p
+    if args.only is not None:
+        print(json.dumps({k: round(v, 5) for k, v in result.items()}))
+        return
+
+    ms = result["ms"]
+    per_call_bytes = decode_bytes(n)
+    value = LAYERS * per_call_bytes / (ms * 1e-3) / 1e9
+    partial_us = result["ms_partial"] * 1e3 / LAYERS
+    achieved = per_call_bytes / (partial_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "us_per_call": round(ms * 1e3 / LAYERS, 3),
+        "frac_of_peak": round(value / PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 storage, f32 accumulate",
+        "data": "synthetic N(0,1) fp16 K/V/Q drawn on the device (seed 2)",
+        "config": {"workload": f"36-layer decode sweep at {n} tokens, Qwen3-4B GQA (32 q / 8 kv heads, D=128), "
+                               f"batch 1, one HIP graph per step",
+                   "layers": LAYERS, "kv_tokens": n, "batch": 1, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "splits": plans[0].splits, "split_tokens": plans[0].split_tokens},
+        "roofline": {"bound": "hbm", "kernel": "decode_partial_kernel<f16, g=4>",
+                     "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "us_per_launch": round(partial_us, 3),
+                     "bytes_per_launch": per_call_bytes,
+                     "traffic": read_traffic(f"decode_partial_n{n}_traffic.txt")},
+    }
+    if not args.no_splice:
+        line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(n, args.cpu_seconds)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

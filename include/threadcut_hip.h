@@ -1,0 +1,169 @@
+/*
+ * threadcut_hip.h — C ABI of the MI355X (gfx950) decode hot path of threadcut.
+ *
+ * Three operations, each a hand-written HIP kernel (or kernel pair):
+ *   - split-KV GQA flash-decode: a partial online-softmax kernel and a separate
+ *     log-sum-exp combine kernel;
+ *   - the RoPE delta-shift of post-RoPE keys (new output buffer);
+ *   - the in-place suffix splice A.B.C -> A.C of every layer of a KV cache,
+ *     fused gather + rotate + store, one launch for all layers.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer argument named *_dev is device memory owned by the caller;
+ *     the library allocates no device memory and keeps no per-call state.
+ *   - Tensors are described by a base pointer plus element strides. The last
+ *     (head_dim) dimension must be contiguous, every base pointer 16-byte
+ *     aligned and every stride a multiple of 8 elements (128-bit accesses).
+ *   - Element type: fp16 (TC_DTYPE_F16) or bf16 (TC_DTYPE_BF16); head_dim 128.
+ *   - `stream` is a hipStream_t (NULL = default stream). Calls only enqueue
+ *     work; none synchronizes the host.
+ *   - Return value: TC_OK (0) or a TC_ERR_* code. Arguments are validated on
+ *     the host before anything is enqueued; tc_last_error() then holds a
+ *     message for the calling thread. No entry point aborts the process.
+ */
+#ifndef THREADCUT_HIP_H
+#define THREADCUT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  TC_OK = 0,
+  TC_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, bad split */
+  TC_ERR_UNSUPPORTED = 2,      /* head_dim / group / dtype outside the kernels */
+  TC_ERR_ALIGNMENT = 3,        /* base or stride not 16-byte aligned */
+  TC_ERR_WORKSPACE = 4,        /* workspace smaller than tc_decode_workspace_bytes */
+  TC_ERR_HIP = 5               /* a HIP runtime call failed (message has details) */
+};
+
+enum { TC_DTYPE_F16 = 0, TC_DTYPE_BF16 = 1 };
+
+/* Largest number of KV splits one decode call may use. */
+#define TC_MAX_SPLITS 4096
+
+/* ------------------------------------------------------------------------ */
+/* Library information                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Static description of a TC_* code. Never NULL. */
+const char* tc_strerror(int code);
+
+/* Message of the last failed call on the calling thread ("" if none). */
+const char* tc_last_error(void);
+
+/* ABI version; bumped on any signature change. */
+int tc_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Split-KV GQA flash-decode                                                 */
+/*                                                                           */
+/* Replaces threadcut/flash_decode.py:57-69 (decode_attention: the Triton    */
+/* `_partial` launch at :64-67 and the torch softmax(lse)-weighted merge at  */
+/* :68-69) and the decode branch of threadcut/attention.py:35-42.            */
+/*                                                                           */
+/* Shapes: q [B, Hkv, G, D] (the G query heads of KV head h are rows         */
+/* h*G .. h*G+G-1 of the model's query heads); k, v [B, Hkv, N, D] where N   */
+/* is the buffer's token capacity; lens[b] (optional) is the number of valid */
+/* tokens of sequence b, otherwise every sequence has n_tokens tokens. The   */
+/* output is [B, Hkv, G, D] with element strides out_strides, in the input   */
+/* dtype, fp32 accumulation throughout.                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Number of KV splits a call with these sizes uses. split_tokens <= 0 lets
+ * the library choose the split length so that B*Hkv*S work-groups fill the
+ * device; a positive value is rounded up to the kernel's token granule (64).
+ * Host-only; needs no GPU when split_tokens > 0. */
+int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_tokens);
+
+/* Tokens per split that a call with these sizes uses (see above). */
+int tc_decode_split_tokens(int batch, int kv_heads, int64_t max_tokens, int split_tokens);
+
+/* Bytes of device workspace for num_splits splits: fp32 partial outputs
+ * [B, Hkv, S, G, D] followed by fp32 partial log-sum-exps [B, Hkv, S, G]. */
+size_t tc_decode_workspace_bytes(int batch, int kv_heads, int group, int head_dim, int num_splits);
+
+/* Partial pass only: writes o_part [B,Hkv,S,G,D] and lse_part [B,Hkv,S,G]
+ * (natural log, -inf for a split without tokens). Equivalent of the Triton
+ * `_partial` kernel, threadcut/flash_decode.py:21-54. */
+int tc_decode_partial(const void* q_dev, const int64_t q_strides[3],
+                      const void* k_dev, const int64_t k_strides[3],
+                      const void* v_dev, const int64_t v_strides[3],
+                      const int32_t* lens_dev, int64_t n_tokens,
+                      int batch, int kv_heads, int group, int head_dim, int dtype,
+                      float scale, int split_tokens, int num_splits,
+                      float* o_part_dev, float* lse_part_dev, void* stream);
+
+/* Combine pass only: out[b,h,g,:] = sum_s softmax_s(lse)[s] * o_part[b,h,s,g,:],
+ * cast to dtype (round to nearest even). All-(-inf) lse (no tokens) gives 0.
+ * Equivalent of threadcut/flash_decode.py:68-69. */
+int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev,
+                      int batch, int kv_heads, int group, int head_dim, int num_splits,
+                      void* out_dev, const int64_t out_strides[3], int dtype, void* stream);
+
+/* Both passes. workspace_dev must hold tc_decode_workspace_bytes(...) bytes
+ * for the split count tc_decode_num_splits(batch, kv_heads, max_tokens,
+ * split_tokens) where max_tokens = n_tokens. With lens_dev != NULL every
+ * lens[b] must be in [0, n_tokens]. */
+int tc_decode_attention(const void* q_dev, const int64_t q_strides[3],
+                        const void* k_dev, const int64_t k_strides[3],
+                        const void* v_dev, const int64_t v_strides[3],
+                        const int32_t* lens_dev, int64_t n_tokens,
+                        int batch, int kv_heads, int group, int head_dim, int dtype,
+                        float scale, int split_tokens,
+                        void* workspace_dev, size_t workspace_bytes,
+                        void* out_dev, const int64_t out_strides[3], void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* RoPE delta-shift and suffix splice                                        */
+/*                                                                           */
+/* cos_sin_host: 2*(head_dim/2) fp32 values on the HOST, cos(angle_i) then   */
+/* sin(angle_i) for i < head_dim/2, angle_i = delta * inv_freq_i, exactly as */
+/* threadcut/kv.py:22-23 builds `emb` (emb = cat(angle, angle), so the upper */
+/* half reuses the same values). The table travels in the kernel arguments.  */
+/* Per element: out = fp16(fl(k*cos) + fl(rotate_half(k)*sin)), no fused     */
+/* multiply-add, matching threadcut/kv.py:25 op for op.                      */
+/* ------------------------------------------------------------------------ */
+
+/* keys [B, H, T, D] (strides src_strides) -> out [B, H, T, D] (strides
+ * dst_strides). out may not alias keys. Replaces threadcut/kv.py:20-25
+ * (shift_keys). */
+int tc_shift_keys(const void* keys_dev, const int64_t src_strides[3],
+                  void* out_dev, const int64_t dst_strides[3],
+                  int batch, int heads, int64_t tokens, int head_dim, int dtype,
+                  const float* cos_sin_host, void* stream);
+
+/* In place, for every layer l < num_layers, every batch row and head:
+ *   K[a + t] <- shift(K[c0 + t]),  V[a + t] <- V[c0 + t]   for t < c
+ * with the memmove semantics of the reference's clone-then-write (sources
+ * are read before they are overwritten, also when c0 - a < c). Rows outside
+ * [a, a+c) are not touched. k_layers_host / v_layers_host are HOST arrays of
+ * num_layers device pointers to [B, H, cap, D] buffers that share `strides`.
+ * c0 == a (no gap) or c == 0 enqueues nothing. cos_sin_host may be NULL
+ * only then. Replaces threadcut/kv.py:28-33 + :83-92 (splice over
+ * GrowingLayer.splice, 36 per-layer torch op chains) with one launch. */
+int tc_splice_rope(void* const* k_layers_host, void* const* v_layers_host, int num_layers,
+                   const int64_t strides[3], int batch, int heads, int64_t capacity,
+                   int head_dim, int dtype, int64_t a, int64_t c0, int64_t c,
+                   const float* cos_sin_host, void* stream);
+
+/* Out of place: for every layer, rows [0, a) of src are copied to rows
+ * [0, a) of dst, and rows [c0, c0+c) of src to rows [a, a+c) of dst, keys
+ * shifted. This is the index_select branch of threadcut/kv.py:34-41 for
+ * caches whose layers are not preallocated buffers. dst must not alias src. */
+int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
+                   const int64_t src_strides[3], int64_t src_tokens,
+                   void* const* k_dst_host, void* const* v_dst_host,
+                   const int64_t dst_strides[3], int num_layers,
+                   int batch, int heads, int head_dim, int dtype,
+                   int64_t a, int64_t c0, int64_t c,
+                   const float* cos_sin_host, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THREADCUT_HIP_H */

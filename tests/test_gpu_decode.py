@@ -1,0 +1,197 @@
+"""Decode parity on the GPU: HIP kernels vs the CPU oracle on the same seeded inputs.
+
+Tolerance (fp16/bf16 outputs after fp32 accumulation): max-abs 2e-3 against
+the float64 closed form / fp32 SDPA; fp32 partials within 1e-4 of the
+restated split-KV kernel at the same split length.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+from threadcut_amd import _lib, attention, flash_decode, workloads
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+SCALE = 128 ** -0.5
+
+
+def f64_ref(q, k, v, scale=SCALE, lens=None):
+    """q [B,Hq,1,D] torch (cpu), k/v [B,Hkv,N,D] -> float64 [B,Hkv,G,D]."""
+    b, hq, _, d = q.shape
+    hkv = k.shape[1]
+    qn = q.float().numpy().reshape(b, hkv, hq // hkv, d)
+    kn, vn = k.float().numpy(), v.float().numpy()
+    if lens is None:
+        return od.attention_f64(qn, kn, vn, scale)
+    return od.decode_ragged(qn, kn, vn, lens.numpy(), scale)
+
+
+def run_decode(q, k, v, dev, scale=SCALE, lens=None, split=None):
+    b, hq, _, d = q.shape
+    hkv = k.shape[1]
+    qd = q.to(dev).reshape(b, hkv, hq // hkv, d)
+    out = flash_decode.decode_attention_batched(qd, k.to(dev), v.to(dev), scale,
+                                                lens=None if lens is None else lens.to(dev), split=split)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def test_single_call_shape_vs_fp32_sdpa(gpu):
+    """Q [1,32,1,128], K/V [1,8,1536,128] fp16, seed 0, against torch SDPA in fp32."""
+    q, k, v, _ = workloads.decode_inputs(0, n=1536)
+    print("case: single call n=1536 seed 0", flush=True)
+    out, none = attention.attention(None, q.to(gpu), k.to(gpu), v.to(gpu), None, scaling=SCALE)
+    torch.cuda.synchronize()
+    assert none is None and out.shape == (1, 1, 32, 128) and out.is_contiguous()
+    ref = od.folded_sdpa(q.float(), k.float(), v.float(), SCALE).transpose(1, 2)
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= TOL, err
+    ref64 = f64_ref(q, k, v).reshape(1, 1, 32, 128)
+    assert np.abs(out.float().cpu().numpy() - ref64).max() <= TOL
+
+
+@pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 63, 64, 65, 100, 255, 256, 257, 1000, 1536, 4096])
+@pytest.mark.parametrize("split", [None, 64, 256])
+def test_lengths_and_splits(gpu, n, split):
+    q, k, v, _ = workloads.decode_inputs(100 + n, n=n)
+    print(f"case: n={n} split={split}", flush=True)
+    got = run_decode(q, k, v, gpu, split=split)
+    assert np.abs(got - f64_ref(q, k, v)).max() <= TOL
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (24, 8), (32, 8), (40, 8), (64, 8), (32, 4), (14, 2)])
+def test_group_sizes(gpu, hq, hkv):
+    q, k, v, _ = workloads.decode_inputs(7, n=777, q_heads=hq, kv_heads=hkv)
+    print(f"case: hq={hq} hkv={hkv}", flush=True)
+    got = run_decode(q, k, v, gpu)
+    assert np.abs(got - f64_ref(q, k, v)).max() <= TOL
+
+
+def test_bf16(gpu):
+    q, k, v, _ = workloads.decode_inputs(8, n=3000, dtype=torch.bfloat16)
+    got = run_decode(q, k, v, gpu)
+    # bf16 output rounding: half an ulp of bf16 at |out| < 1 is 2^-9.
+    assert np.abs(got - f64_ref(q, k, v)).max() <= 4e-3
+
+
+def test_partials_match_restated_kernel(gpu):
+    """o_part / lse_part at split 256 against the restated Triton program."""
+    q, k, v, _ = workloads.decode_inputs(9, n=1000)
+    hkv, g, d = 8, 4, 128
+    qd = q.to(gpu).reshape(1, hkv, g, d)
+    kd, vd = k.to(gpu), v.to(gpu)
+    S = flash_decode.num_splits(1, hkv, 1000, 256)
+    assert S == 4
+    o = torch.empty((1, hkv, S, g, d), dtype=torch.float32, device=gpu)
+    lse = torch.empty((1, hkv, S, g), dtype=torch.float32, device=gpu)
+    lib = _lib.load()
+    rc = lib.tc_decode_partial(qd.data_ptr(), _lib.i64x3(*qd.stride()[:3]), kd.data_ptr(), _lib.i64x3(*kd.stride()[:3]),
+                               vd.data_ptr(), _lib.i64x3(*vd.stride()[:3]), None, 1000, 1, hkv, g, d,
+                               _lib.TC_DTYPE_F16, SCALE, 256, S, o.data_ptr(), lse.data_ptr(),
+                               _lib.stream_of(gpu))
+    _lib.check(rc, "tc_decode_partial")
+    torch.cuda.synchronize()
+    ro, rl = od.flash_decode_partial(q.float().numpy().reshape(hkv, g, d), k[0].float().numpy(),
+                                     v[0].float().numpy(), SCALE, split=256)
+    assert np.abs(o[0].permute(1, 0, 2, 3).cpu().numpy() - ro).max() <= 1e-4
+    assert np.abs(lse[0].permute(1, 0, 2).cpu().numpy() - rl).max() <= 1e-4
+    # Combine alone on the oracle's partials.
+    out = torch.empty((1, hkv, g, d), dtype=torch.float16, device=gpu)
+    o2 = torch.from_numpy(ro).permute(1, 0, 2, 3).contiguous()[None].to(gpu)
+    l2 = torch.from_numpy(rl).permute(1, 0, 2).contiguous()[None].to(gpu)
+    rc = lib.tc_decode_combine(o2.data_ptr(), l2.data_ptr(), 1, hkv, g, d, S, out.data_ptr(),
+                               _lib.i64x3(*out.stride()[:3]), _lib.TC_DTYPE_F16, _lib.stream_of(gpu))
+    _lib.check(rc, "tc_decode_combine")
+    torch.cuda.synchronize()
+    comb = od.flash_decode_combine(ro, rl)
+    assert np.abs(out[0].float().cpu().numpy() - comb).max() <= 1e-3
+
+
+def test_empty_cache_gives_zeros(gpu):
+    q, k, v, _ = workloads.decode_inputs(10, n=0)
+    got = run_decode(q, k, v, gpu)
+    assert got.shape == (1, 8, 4, 128) and np.all(got == 0)
+
+
+def test_strided_cache_views_and_transposed_query(gpu):
+    """K/V as views [..., :n, :] of a larger buffer; q as the transposed [b, hq, 1, d] view."""
+    cap, n = 5000, 3333
+    g_ = torch.Generator().manual_seed(11)
+    kbuf = torch.randn(1, 8, cap, 128, generator=g_).half().to(gpu)
+    vbuf = torch.randn(1, 8, cap, 128, generator=g_).half().to(gpu)
+    qflat = torch.randn(1, 1, 32, 128, generator=g_).half().to(gpu)
+    query = qflat.transpose(1, 2)  # [1, 32, 1, 128], strides of a transpose
+    out, _ = attention.attention(None, query, kbuf[:, :, :n], vbuf[:, :, :n], None, scaling=SCALE)
+    torch.cuda.synchronize()
+    ref = f64_ref(query.cpu(), kbuf[:, :, :n].cpu(), vbuf[:, :, :n].cpu()).reshape(1, 1, 32, 128)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL
+
+
+def test_large_scores_stay_finite(gpu):
+    """q scaled by 10: scores of ~N(0, 100), a peaked softmax."""
+    q, k, v, _ = workloads.decode_inputs(12, n=2048)
+    q = (q.float() * 10).half()
+    got = run_decode(q, k, v, gpu)
+    assert np.isfinite(got).all()
+    assert np.abs(got - f64_ref(q, k, v)).max() <= TOL
+
+
+def test_constant_values_and_zero_query(gpu):
+    q, k, v, _ = workloads.decode_inputs(13, n=900)
+    v_const = v.clone()
+    v_const[:] = v[:, :, 5:6, :]
+    got = run_decode(q, k, v_const, gpu)
+    row = v[:, :, 5, :].float().numpy()[:, :, None, :]
+    assert np.abs(got - row).max() <= TOL
+    got0 = run_decode(torch.zeros_like(q), k, v, gpu)
+    mean = v.float().numpy().mean(axis=2)[:, :, None, :]
+    assert np.abs(got0 - mean).max() <= TOL
+
+
+def test_ragged_batch_sixteen_sequences(gpu):
+    """16 sequences, lengths U[1024, 32768] (seed 3), padded cache + int32 lengths."""
+    q, k, v, lens = workloads.decode_inputs(3, batch=16, n=32768, lens_range=(1024, 32768))
+    print(f"case: ragged B=16 lens={lens.tolist()}", flush=True)
+    got = run_decode(q, k, v, gpu, lens=lens)
+    ref = f64_ref(q, k, v, lens=lens)
+    assert np.abs(got - ref).max() <= TOL
+
+
+def test_ragged_with_empty_and_full_rows(gpu):
+    q, k, v, _ = workloads.decode_inputs(14, batch=4, n=700)
+    lens = torch.tensor([0, 1, 699, 700], dtype=torch.int32)
+    got = run_decode(q, k, v, gpu, lens=lens)
+    ref = f64_ref(q, k, v, lens=lens)
+    assert np.all(got[0] == 0)
+    assert np.abs(got - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_long_context_131072(gpu, batch):
+    """131072 tokens (seed 4): many splits and the LSE combine, vs fp32 SDPA on the CPU."""
+    q, k, v, _ = workloads.decode_inputs(4, batch=batch, n=131072)
+    print(f"case: long context B={batch} n=131072", flush=True)
+    got = run_decode(q, k, v, gpu)
+    ref = od.folded_sdpa(q.float(), k.float(), v.float(), SCALE).reshape(batch, 8, 4, 128).numpy()
+    assert np.abs(got - ref).max() <= TOL
+
+
+def test_decode_attention_signature(gpu):
+    """flash_decode.decode_attention(q [hkv,g,d], k, v [hkv,n,d], scale, split, block)."""
+    q, k, v, _ = workloads.decode_inputs(15, n=1300)
+    out = flash_decode.decode_attention(q.to(gpu).reshape(8, 4, 128), k[0].to(gpu), v[0].to(gpu), SCALE,
+                                        split=256, block=16)
+    torch.cuda.synchronize()
+    assert out.shape == (8, 4, 128) and out.dtype == torch.float16
+    assert np.abs(out.float().cpu().numpy() - f64_ref(q, k, v)[0]).max() <= TOL
+
+
+def test_rejects_bad_inputs(gpu):
+    q, k, v, _ = workloads.decode_inputs(16, n=64, head_dim=64)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        run_decode(q, k, v, gpu)
+    q, k, v, _ = workloads.decode_inputs(16, n=64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        flash_decode.decode_attention(q.reshape(8, 4, 128), k[0], v[0], SCALE)

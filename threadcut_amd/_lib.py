@@ -1,0 +1,116 @@
+"""ctypes binding of ``libthreadcut_hip.so`` (declared in include/threadcut_hip.h).
+
+The library is built in-tree by ``threadcut_amd.build``. Loading it is the
+only way to reach the kernels: there is no fallback, and a missing library
+raises ``RuntimeError`` naming the build command.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libthreadcut_hip.so")
+
+TC_OK = 0
+TC_ERR_INVALID_ARGUMENT = 1
+TC_ERR_UNSUPPORTED = 2
+TC_ERR_ALIGNMENT = 3
+TC_ERR_WORKSPACE = 4
+TC_ERR_HIP = 5
+
+TC_DTYPE_F16 = 0
+TC_DTYPE_BF16 = 1
+TC_MAX_SPLITS = 4096
+
+_DTYPES = {torch.float16: TC_DTYPE_F16, torch.bfloat16: TC_DTYPE_BF16}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_S = ctypes.c_size_t
+_I64P = ctypes.POINTER(ctypes.c_int64)
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_FP = ctypes.POINTER(ctypes.c_float)
+
+# name -> (restype, argtypes); every extern "C" symbol of the header.
+SIGNATURES = {
+    "tc_strerror": (ctypes.c_char_p, [_I]),
+    "tc_last_error": (ctypes.c_char_p, []),
+    "tc_abi_version": (_I, []),
+    "tc_decode_num_splits": (_I, [_I, _I, _I64, _I]),
+    "tc_decode_split_tokens": (_I, [_I, _I, _I64, _I]),
+    "tc_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
+    "tc_decode_partial": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I,
+                               _P, _P, _P]),
+    "tc_decode_combine": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _I64P, _I, _P]),
+    "tc_decode_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
+                                 _P, _S, _P, _I64P, _P]),
+    "tc_shift_keys": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I64, _I, _I, _FP, _P]),
+    "tc_splice_rope": (_I, [_PP, _PP, _I, _I64P, _I, _I, _I64, _I, _I, _I64, _I64, _I64, _FP, _P]),
+    "tc_splice_copy": (_I, [_PP, _PP, _I64P, _I64, _PP, _PP, _I64P, _I, _I, _I, _I, _I, _I64, _I64, _I64,
+                            _FP, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """The loaded library (loaded once). Raises RuntimeError if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"threadcut_amd: {LIB_PATH} is missing; build it with `python -m threadcut_amd.build` "
+                    "(or __graft_entry__.build()). There is no fallback path.")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(rc, what):
+    """Raise RuntimeError with the library's message unless rc == TC_OK."""
+    if rc != TC_OK:
+        lib = load()
+        msg = lib.tc_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {lib.tc_strerror(rc).decode()} ({msg})")
+
+
+def dtype_code(t):
+    try:
+        return _DTYPES[t]
+    except KeyError:
+        raise TypeError(f"threadcut_amd kernels take float16 or bfloat16 tensors, got {t}") from None
+
+
+def i64x3(a, b, c):
+    return (ctypes.c_int64 * 3)(int(a), int(b), int(c))
+
+
+def ptr_array(ptrs):
+    return (ctypes.c_void_p * max(1, len(ptrs)))(*[ctypes.c_void_p(int(p)) for p in ptrs])
+
+
+def float_array(t):
+    """Host fp32 array from a CPU float32 tensor (kept alive by the caller)."""
+    t = t.detach().to("cpu", torch.float32).contiguous()
+    return (ctypes.c_float * t.numel())(*t.tolist())
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*tensors, what):
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(f"{what}: threadcut_amd runs on the GPU (HIP) only; got a {t.device} tensor")

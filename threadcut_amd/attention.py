@@ -1,0 +1,51 @@
+"""GQA-aware attention registered into transformers as ``"threadcut"``.
+
+Drop-in for threadcut/attention.py:22-51. Decode (one query token, no mask):
+the g query heads sharing a KV head are handed to the split-KV HIP kernels of
+``flash_decode`` together with the unexpanded cache views, for any batch
+size (the reference used its GPU kernel for b == 1 and SDPA otherwise; both
+compute the same softmax). Prefill keeps the reference's path: expand KV once
+and run SDPA with the mask (threadcut/attention.py:43-46); it is not part of
+the decode hot path.
+"""
+import torch
+import torch.nn.functional as F
+from transformers import AttentionInterface
+from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+
+from .flash_decode import decode_into
+
+NAME = "threadcut"
+
+
+def repeat_kv(x, n):
+    """[b, h, s, d] -> [b, h*n, s, d], each KV head repeated n times in place order."""
+    if n == 1:
+        return x
+    b, h, s, d = x.shape
+    return x.unsqueeze(2).expand(b, h, n, s, d).reshape(b, h * n, s, d)
+
+
+def attention(module, query, key, value, attention_mask, dropout=0.0, scaling=None, **kwargs):
+    """transformers attention interface (threadcut/attention.py:30-47).
+
+    query [b, hq, q, d] (usually a transposed view), key/value [b, hkv, n, d]
+    (views into the cache). Returns ([b, q, hq, d] contiguous, None).
+    """
+    b, hq, q, d = query.shape
+    hkv = key.shape[1]
+    g = hq // hkv
+    scaling = scaling if scaling is not None else d ** -0.5
+    if q == 1 and attention_mask is None:
+        # [b, 1, hq, d] contiguous is [b, hkv, g, d] with head index h*g + i.
+        out = torch.empty((b, 1, hq, d), dtype=query.dtype, device=query.device)
+        decode_into(query.reshape(b, hkv, g, d), key, value, scaling, out.view(b, hkv, g, d))
+        return out, None
+    is_causal = attention_mask is None and q > 1 and q == key.shape[2]
+    out = F.scaled_dot_product_attention(query, repeat_kv(key, g), repeat_kv(value, g),
+                                         attn_mask=attention_mask, scale=scaling, is_causal=is_causal)
+    return out.transpose(1, 2).contiguous(), None
+
+
+AttentionInterface.register(NAME, attention)
+AttentionMaskInterface.register(NAME, sdpa_mask)

@@ -1,0 +1,65 @@
+"""Build recipe of the threadcut HIP library (gfx950 only).
+
+Compiles every ``csrc/*.hip`` source with hipcc into ``_build/*.o`` (in
+parallel) and links ``libthreadcut_hip.so`` next to this file, where
+``threadcut_amd._lib`` loads it. Run as ``python -m threadcut_amd.build``.
+"""
+import concurrent.futures
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libthreadcut_hip.so")
+ARCH = "gfx950"
+
+# Packed-fp32 VALU forms stay off: the kernels are written for scalar fp32.
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def hipcc():
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found (needs ROCm)")
+    return path
+
+
+def _compile(src, obj):
+    cmd = [hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass reports the device-only feature flag as unknown; drop that noise.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(line for line in r.stderr.splitlines() if noise not in line)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n{err}")
+    return err
+
+
+def build(verbose=False):
+    """Compile and link the library; returns its path. Always rebuilds."""
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    objs = [os.path.join(BUILD, os.path.basename(s)[:-4] + ".o") for s in sources]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
+        for src, warn in zip(sources, ex.map(_compile, sources, objs)):
+            if warn and verbose:
+                print(f"[{os.path.basename(src)}]\n{warn}", file=sys.stderr)
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,672 @@
+// Split-KV GQA flash-decode for gfx950: a partial online-softmax kernel over
+// (split, kv head, sequence) work-groups and a separate log-sum-exp combine.
+//
+// Reference semantics: threadcut/flash_decode.py:21-54 (`_partial`: fp32
+// math, scale applied after q.k, -inf guards, out = acc / l, lse = m + log l)
+// and :57-69 (decode_attention: splits = cdiv(n, split), merge with
+// softmax(lse) weights, cast to q.dtype).
+//
+// Layout of one wave64 over the cache: a 16-token iteration issues four
+// 1 KiB-contiguous 128-bit loads of K (and four of V). Lane l reads token
+// t0 + 4j + (l >> 4), dims 8*(l & 15) .. +8, for j = 0..3, so the wave's 16
+// lanes of a row hold one token and the four rows hold four tokens. The g
+// query heads of the KV head stay in registers and share every K/V element.
+//   - q.k: v_dot2_f32_{f16,bf16} over the lane's 8 dims, then a DPP
+//     reduce-scatter inside each row (4 steps) leaves every lane with the full
+//     score of one (token, head) pair (two for g > 4);
+//   - online softmax per row and head in the log2 domain (exp2), max via two
+//     DPP steps over the four lanes of a head;
+//   - p.v: each lane accumulates its 8 dims for the row's token, p broadcast
+//     from the owning lane with DPP row_newbcast.
+// Four rows x four waves are independent online-softmax streams; they are
+// merged once at the end (cross-row shuffles, then LDS across waves) so each
+// work-group writes one (o, lse) partial per query head.
+#include <math.h>
+
+#include "tc_common.hpp"
+
+namespace tc {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kWaves = 4;                            // waves per work-group
+constexpr int kWaveIter = 16;                        // tokens per wave iteration
+constexpr int kSplitGranule = kWaves * kWaveIter;    // split length granule
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct PartialArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  float* o_part;       // [B, H, S, G, D]
+  float* lse_part;     // [B, H, S, G]
+  const int32_t* lens; // [B] or null
+  int64_t n;
+  int64_t sq_b, sq_h, sq_g;
+  int64_t sk_b, sk_h, sk_t;
+  int64_t sv_b, sv_h, sv_t;
+  int heads, group, splits, split_tokens;
+  float scale_log2;    // softmax scale * log2(e)
+};
+
+struct CombineArgs {
+  const float* o_part;
+  const float* lse_part;
+  uint16_t* out;
+  int64_t so_b, so_h, so_g;
+  int heads, group, splits;
+};
+
+__device__ __forceinline__ uint4 load16(const uint16_t* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& x, int i) {
+  return i == 0 ? x.x : (i == 1 ? x.y : (i == 2 ? x.z : x.w));
+}
+
+// Lane permutations that make the row reduction select-free.
+//
+// A lane's partial dots are x[slot' * GP + head'] (slot' < 4, head' < GP):
+// K register slot' holds token slot slot' ^ (c >> 2) of the iteration and q
+// register head' holds query row head' ^ head_perm(c). Written as a bit
+// vector, register r of lane c then carries value r ^ X(c), where X is the
+// linear map that sends the DPP partner patterns used below (c ^ 8, c ^ 7
+// via half-mirror, c ^ 2, c ^ 1) to the register bits halved at each step.
+// Every step is x[i] += dpp(x[i + K/2]) on all lanes: no per-lane selects.
+template <int GP>
+__device__ __forceinline__ int head_perm(int c) {
+  const int flip = ((c >> 2) & 1) ? 3 : 0;
+  if constexpr (GP == 1) return 0;
+  else if constexpr (GP == 2) return ((c >> 1) & 1) ^ ((c >> 2) & 1);
+  else if constexpr (GP == 4) return (c & 3) ^ flip;
+  else return 2 * ((c & 3) ^ flip);
+}
+
+// Row lane holding the score of (token slot j, head hh) after the scatter.
+template <int GP>
+constexpr int owner_lane(int j, int hh) {
+  return GP == 1 ? 4 * j
+       : GP == 2 ? 4 * j + 2 * (hh ^ (j & 1))
+       : GP == 4 ? 4 * j + (hh ^ ((j & 1) ? 3 : 0))
+                 : 4 * j + ((hh >> 1) ^ ((j & 1) ? 3 : 0));
+}
+
+// Register (index < VPL) of that lane holding it.
+template <int GP>
+constexpr int owner_reg(int hh) { return GP == 8 ? (hh & 1) : 0; }
+
+// Sum of the NV = 4 * GP partial dots over the 16 lanes of each row,
+// scattered: lane c keeps the totals of its first VPL registers.
+template <int NV>
+__device__ __forceinline__ void row_reduce_scatter(float* x) {
+#pragma unroll
+  for (int i = 0; i < NV / 2; ++i) x[i] += dpp<DPP_ROW_ROR8>(x[i + NV / 2]);
+#pragma unroll
+  for (int i = 0; i < NV / 4; ++i) x[i] += dpp<DPP_ROW_HALF_MIRROR>(x[i + NV / 4]);
+  if constexpr (NV / 8 >= 1) {
+#pragma unroll
+    for (int i = 0; i < NV / 8; ++i) x[i] += dpp<DPP_QUAD_XOR2>(x[i + NV / 8]);
+  } else {
+    x[0] += dpp<DPP_QUAD_XOR2>(x[0]);
+  }
+  if constexpr (NV / 16 >= 1) {
+#pragma unroll
+    for (int i = 0; i < NV / 16; ++i) x[i] += dpp<DPP_QUAD_XOR1>(x[i + NV / 16]);
+  } else {
+    x[0] += dpp<DPP_QUAD_XOR1>(x[0]);
+  }
+}
+
+// All-reduce over the four lanes of a row that own one head (c, c^8, c^7, c^15).
+__device__ __forceinline__ float head_max(float t) {
+  t = fmaxf(t, dpp<DPP_ROW_ROR8>(t));
+  return fmaxf(t, dpp<DPP_ROW_HALF_MIRROR>(t));
+}
+__device__ __forceinline__ float head_sum(float t) {
+  t += dpp<DPP_ROW_ROR8>(t);
+  return t + dpp<DPP_ROW_HALF_MIRROR>(t);
+}
+
+// Value of x held by lane k of the caller's row; k folds to a constant after
+// unrolling, so the switch reduces to one DPP move.
+__device__ __forceinline__ float row_bcast_dyn(float x, int k) {
+  switch (k) {
+    case 0: return row_bcast<0>(x);
+    case 1: return row_bcast<1>(x);
+    case 2: return row_bcast<2>(x);
+    case 3: return row_bcast<3>(x);
+    case 4: return row_bcast<4>(x);
+    case 5: return row_bcast<5>(x);
+    case 6: return row_bcast<6>(x);
+    case 7: return row_bcast<7>(x);
+    case 8: return row_bcast<8>(x);
+    case 9: return row_bcast<9>(x);
+    case 10: return row_bcast<10>(x);
+    case 11: return row_bcast<11>(x);
+    case 12: return row_bcast<12>(x);
+    case 13: return row_bcast<13>(x);
+    case 14: return row_bcast<14>(x);
+    default: return row_bcast<15>(x);
+  }
+}
+
+template <int GP>
+__device__ __forceinline__ float owner_bcast(const float* x, int j, int hh) {
+  return row_bcast_dyn(x[owner_reg<GP>(hh)], owner_lane<GP>(j, hh));
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource over `bytes` bytes at p; loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// K/V rows of one 16-token iteration of a wave: rows at or past `end` read
+// as zero (their scores are masked), so no index clamping is needed.
+struct Tile {
+  uint4 k[4];  // register j: token slot j ^ (c >> 2)
+  uint4 v[4];  // register j: token slot j
+};
+
+__device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char* vslab, int64_t row_k,
+                                          int64_t row_v, int64_t t0, int64_t end, const int32_t* koff,
+                                          const int32_t* voff) {
+  const int64_t rows = min(max(end - t0, int64_t(0)), int64_t(16));
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kslab + t0 * row_k, static_cast<int32_t>(rows * row_k));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vslab + t0 * row_v, static_cast<int32_t>(rows * row_v));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    t.k[j] = bload16(rk, koff[j]);
+    t.v[j] = bload16(rv, voff[j]);
+  }
+}
+
+template <int DT, int GP>
+struct Stream {
+  static constexpr int NV = 4 * GP;                   // partial dots per lane per iteration
+  static constexpr int VPL = NV >= 16 ? NV / 16 : 1;  // scores owned per lane
+  float m[VPL];          // running max (log2 domain) of the lane's head(s), per row
+  float l[VPL];          // running sum of exp2(score - m) over the lane's token slot
+  float acc[GP][8];      // running p.v for the lane's 8 dims, every head
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) { m[i] = neg_inf(); l[i] = 0.f; }
+#pragma unroll
+    for (int hh = 0; hh < GP; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[hh][e] = 0.f;
+  }
+
+  // One 16-token iteration; `valid` masks the lane's score(s).
+  __device__ __forceinline__ void step(const Tile& t, const uint32_t (&qw)[GP][4], bool valid, float scale_log2) {
+    using E = Elem<DT>;
+    float x[NV];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int hh = 0; hh < GP; ++hh) {
+        float d = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) d = E::dot2(word(t.k[j], w), qw[hh][w], d);
+        x[j * GP + hh] = d;
+      }
+    row_reduce_scatter<NV>(x);
+
+    float p[VPL], alpha[VPL];
+    bool rescale = false;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const float s = valid ? x[i] * scale_log2 : neg_inf();
+      const float mn = fmaxf(m[i], head_max(s));
+      const float ms = (mn == neg_inf()) ? 0.f : mn;
+      p[i] = __builtin_amdgcn_exp2f(s - ms);
+      alpha[i] = __builtin_amdgcn_exp2f(m[i] - ms);
+      rescale |= (mn != m[i]) && (m[i] != neg_inf());
+      l[i] = l[i] * alpha[i] + p[i];
+      m[i] = mn;
+    }
+    if (__any(rescale)) {
+#pragma unroll
+      for (int hh = 0; hh < GP; ++hh) {
+        const float ah = owner_bcast<GP>(alpha, 0, hh);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[hh][e] *= ah;
+      }
+    }
+
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float vf[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        vf[2 * w] = E::lo(word(t.v[j], w));
+        vf[2 * w + 1] = E::hi(word(t.v[j], w));
+      }
+#pragma unroll
+      for (int hh = 0; hh < GP; ++hh) {
+        const float pj = owner_bcast<GP>(p, j, hh);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(pj, vf[e], acc[hh][e]);
+      }
+    }
+  }
+};
+
+template <int DT, int GP>
+__global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const PartialArgs a) {
+  __shared__ float s_acc[kWaves][GP][kHeadDim];
+  __shared__ float s_m[kWaves][GP];
+  __shared__ float s_l[kWaves][GP];
+
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep the
+  // token range (and so the buffer resources) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = lane >> 4;
+  const int c = lane & 15;
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+
+  // Lengths past the buffer (or negative) are clamped into [0, n].
+  const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), a.n) : a.n;
+  const int wave_tokens = a.split_tokens / kWaves;
+  const int64_t start = static_cast<int64_t>(split) * a.split_tokens +
+                        static_cast<int64_t>(wave) * wave_tokens;
+  const int64_t end = min(start + wave_tokens, len);
+
+  // The lane's 8 dims of every query row, in the lane's head order.
+  uint32_t qw[GP][4];
+  {
+    const uint16_t* qb = a.q + b * a.sq_b + h * a.sq_h + 8 * c;
+    const int hp = head_perm<GP>(c);
+#pragma unroll
+    for (int hh = 0; hh < GP; ++hh) {
+      const int row = hh ^ hp;
+      uint4 t = make_uint4(0u, 0u, 0u, 0u);
+      if (row < a.group) t = *reinterpret_cast<const uint4*>(qb + row * a.sq_g);
+      qw[hh][0] = t.x; qw[hh][1] = t.y; qw[hh][2] = t.z; qw[hh][3] = t.w;
+    }
+  }
+
+  const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
+  const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
+  const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
+  int32_t koff[4], voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    koff[j] = static_cast<int32_t>((4 * (j ^ (c >> 2)) + grp) * row_k + 16 * c);
+    voff[j] = static_cast<int32_t>((4 * j + grp) * row_v + 16 * c);
+  }
+
+  Stream<DT, GP> st;
+  st.init();
+  const int my_slot = 4 * (c >> 2) + grp;  // token slot of the lane's score(s)
+
+  if (start < end) {
+    Tile t0, t1;
+    load_tile(t0, kslab, vslab, row_k, row_v, start, end, koff, voff);
+    for (int64_t tok = start;; tok += 2 * kWaveIter) {
+      load_tile(t1, kslab, vslab, row_k, row_v, tok + kWaveIter, end, koff, voff);
+      st.step(t0, qw, tok + my_slot < end, a.scale_log2);
+      if (tok + kWaveIter >= end) break;
+      load_tile(t0, kslab, vslab, row_k, row_v, tok + 2 * kWaveIter, end, koff, voff);
+      st.step(t1, qw, tok + kWaveIter + my_slot < end, a.scale_log2);
+      if (tok + 2 * kWaveIter >= end) break;
+    }
+  }
+
+  constexpr int VPL = Stream<DT, GP>::VPL;
+  // Row totals of l over the four token slots of each head, then every
+  // head's (m, l) to every lane.
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) st.l[i] = head_sum(st.l[i]);
+  float mh[GP], lh[GP];
+#pragma unroll
+  for (int hh = 0; hh < GP; ++hh) {
+    mh[hh] = owner_bcast<GP>(st.m, 0, hh);
+    lh[hh] = owner_bcast<GP>(st.l, 0, hh);
+  }
+
+  // Merge the four rows (lanes c, c+16, c+32, c+48 hold the same dims).
+#pragma unroll
+  for (int hh = 0; hh < GP; ++hh) {
+    float M = fmaxf(mh[hh], __shfl_xor(mh[hh], 16));
+    M = fmaxf(M, __shfl_xor(M, 32));
+    const float f = __builtin_amdgcn_exp2f(mh[hh] - ((M == neg_inf()) ? 0.f : M));
+    float L = lh[hh] * f;
+    L += __shfl_xor(L, 16);
+    L += __shfl_xor(L, 32);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float y = st.acc[hh][e] * f;
+      y += __shfl_xor(y, 16);
+      y += __shfl_xor(y, 32);
+      st.acc[hh][e] = y;
+    }
+    mh[hh] = M;
+    lh[hh] = L;
+  }
+
+  // Merge the waves through LDS and write this split's partial.
+  if (grp == 0) {
+#pragma unroll
+    for (int hh = 0; hh < GP; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[wave][hh][8 * c + e] = st.acc[hh][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int hh = 0; hh < GP; ++hh) { s_m[wave][hh] = mh[hh]; s_l[wave][hh] = lh[hh]; }
+  }
+  __syncthreads();
+
+  const int64_t part = (static_cast<int64_t>(b) * a.heads + h) * a.splits + split;
+  for (int idx = threadIdx.x; idx < a.group * kHeadDim; idx += 64 * kWaves) {
+    const int hh = idx / kHeadDim;
+    const int d = idx % kHeadDim;
+    float M = neg_inf();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
+    const float Ms = (M == neg_inf()) ? 0.f : M;
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = __builtin_amdgcn_exp2f(s_m[w][hh] - Ms);
+      L += s_l[w][hh] * f;
+      O += s_acc[w][hh][d] * f;
+    }
+    a.o_part[(part * a.group + hh) * kHeadDim + d] = O / (L == 0.f ? 1.f : L);
+    if (d == 0)
+      a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (M + __log2f(L)) * kLn2;
+  }
+}
+
+// One work-group per (sequence, kv head, query head): weights exp(lse - max)
+// over the splits, 8 split lanes x 32 dim quads accumulate o, LDS reduce.
+template <int DT>
+__global__ __launch_bounds__(256) void decode_combine_kernel(const CombineArgs a) {
+  using E = Elem<DT>;
+  constexpr int kSplitLanes = 8;
+  __shared__ float s_w[TC_MAX_SPLITS];
+  __shared__ float s_red[kWaves];
+  __shared__ float4 s_o[kSplitLanes][kHeadDim / 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int G = a.group;
+  const int S = a.splits;
+  const int64_t bhg = blockIdx.x;
+  const int g = static_cast<int>(bhg % G);
+  const int64_t bh = bhg / G;
+  const int h = static_cast<int>(bh % a.heads);
+  const int64_t b = bh / a.heads;
+
+  const float* lse = a.lse_part + bh * S * G + g;
+  const float* o = a.o_part + (bh * S * G + g) * kHeadDim;
+
+  float mx = neg_inf();
+  for (int s = tid; s < S; s += 256) mx = fmaxf(mx, lse[static_cast<int64_t>(s) * G]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if (lane == 0) s_red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float ms = (mx == neg_inf()) ? 0.f : mx;
+  __syncthreads();
+
+  float sum = 0.f;
+  for (int s = tid; s < S; s += 256) {
+    const float e = __builtin_amdgcn_exp2f((lse[static_cast<int64_t>(s) * G] - ms) * kLog2e);
+    s_w[s] = e;
+    sum += e;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane == 0) s_red[wave] = sum;
+  __syncthreads();
+  sum = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+
+  const int sl = tid >> 5;   // split lane
+  const int dq = tid & 31;   // dims 4*dq .. 4*dq+3
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int s = sl; s < S; s += kSplitLanes) {
+    const float w = s_w[s];
+    const float4 ov = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(s) * G * kHeadDim + 4 * dq);
+    acc.x = fmaf(w, ov.x, acc.x);
+    acc.y = fmaf(w, ov.y, acc.y);
+    acc.z = fmaf(w, ov.z, acc.z);
+    acc.w = fmaf(w, ov.w, acc.w);
+  }
+  s_o[sl][dq] = acc;
+  __syncthreads();
+  if (tid < kHeadDim / 4) {
+    float4 r = s_o[0][tid];
+#pragma unroll
+    for (int k = 1; k < kSplitLanes; ++k) {
+      const float4 t = s_o[k][tid];
+      r.x += t.x; r.y += t.y; r.z += t.z; r.w += t.w;
+    }
+    const bool empty = (mx == neg_inf());
+    const float inv = empty ? 0.f : 1.f / sum;
+    const uint32_t w0 = E::bits(r.x * inv) | (E::bits(r.y * inv) << 16);
+    const uint32_t w1 = E::bits(r.z * inv) | (E::bits(r.w * inv) << 16);
+    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 4 * tid;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side validation and launch.
+// ---------------------------------------------------------------------------
+
+int check_strides(const char* what, const int64_t* st, int n) {
+  if (!st) return fail(TC_ERR_INVALID_ARGUMENT, "%s strides are null", what);
+  for (int i = 0; i < n; ++i) {
+    if (st[i] < 0) return fail(TC_ERR_INVALID_ARGUMENT, "%s stride %d is negative (%lld)", what, i, (long long)st[i]);
+    if (st[i] % 8 != 0)
+      return fail(TC_ERR_ALIGNMENT, "%s stride %d (%lld elements) is not a multiple of 8", what, i, (long long)st[i]);
+  }
+  return TC_OK;
+}
+
+int check_common(int batch, int kv_heads, int group, int head_dim, int dtype) {
+  if (batch < 1 || batch > 65535) return fail(TC_ERR_INVALID_ARGUMENT, "batch %d outside [1, 65535]", batch);
+  if (kv_heads < 1 || kv_heads > 65535) return fail(TC_ERR_INVALID_ARGUMENT, "kv_heads %d outside [1, 65535]", kv_heads);
+  if (group < 1 || group > 8) return fail(TC_ERR_UNSUPPORTED, "group (query heads per KV head) %d outside [1, 8]", group);
+  if (head_dim != kHeadDim) return fail(TC_ERR_UNSUPPORTED, "head_dim %d unsupported (kernels are built for 128)", head_dim);
+  if (dtype != TC_DTYPE_F16 && dtype != TC_DTYPE_BF16) return fail(TC_ERR_UNSUPPORTED, "dtype %d unsupported", dtype);
+  return TC_OK;
+}
+
+template <int DT, int GP>
+hipError_t launch_partial_t(const PartialArgs& a, int batch, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_partial_kernel<DT, GP>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream) {
+  if (a.group <= 1) return launch_partial_t<DT, 1>(a, batch, stream);
+  if (a.group <= 2) return launch_partial_t<DT, 2>(a, batch, stream);
+  if (a.group <= 4) return launch_partial_t<DT, 4>(a, batch, stream);
+  return launch_partial_t<DT, 8>(a, batch, stream);
+}
+
+int split_tokens_impl(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int* out) {
+  if (batch < 1 || kv_heads < 1 || max_tokens < 0)
+    return fail(TC_ERR_INVALID_ARGUMENT, "split query with batch %d, kv_heads %d, max_tokens %lld", batch, kv_heads,
+                (long long)max_tokens);
+  // Shortest split that keeps the split count within TC_MAX_SPLITS.
+  const int64_t floor_t = ceil_div(ceil_div(max_tokens, TC_MAX_SPLITS), kSplitGranule) * kSplitGranule;
+  int64_t t;
+  if (split_tokens > 0) {
+    t = ceil_div(split_tokens, kSplitGranule) * kSplitGranule;
+  } else {
+    int cus = 0;
+    const int rc = current_device_cus(&cus);
+    if (rc != TC_OK) return rc;
+    // About two work-groups per compute unit over all (sequence, head) pairs.
+    const int64_t target = 2 * static_cast<int64_t>(cus);
+    t = ceil_div(ceil_div(max_tokens * batch * kv_heads, target), kSplitGranule) * kSplitGranule;
+  }
+  t = max(t, static_cast<int64_t>(kSplitGranule));
+  t = max(t, floor_t);
+  if (t > (1 << 30)) return fail(TC_ERR_INVALID_ARGUMENT, "split length %lld too large", (long long)t);
+  *out = static_cast<int>(t);
+  return TC_OK;
+}
+
+}  // namespace
+}  // namespace tc
+
+using namespace tc;
+
+extern "C" {
+
+int tc_decode_split_tokens(int batch, int kv_heads, int64_t max_tokens, int split_tokens) {
+  clear_error();
+  int t = 0;
+  const int rc = split_tokens_impl(batch, kv_heads, max_tokens, split_tokens, &t);
+  return rc == TC_OK ? t : -rc;
+}
+
+int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_tokens) {
+  clear_error();
+  int t = 0;
+  const int rc = split_tokens_impl(batch, kv_heads, max_tokens, split_tokens, &t);
+  if (rc != TC_OK) return -rc;
+  return static_cast<int>(ceil_div(max_tokens, t));
+}
+
+size_t tc_decode_workspace_bytes(int batch, int kv_heads, int group, int head_dim, int num_splits) {
+  if (batch < 1 || kv_heads < 1 || group < 1 || head_dim < 1 || num_splits < 0) return 0;
+  const size_t parts = static_cast<size_t>(batch) * kv_heads * num_splits * group;
+  return parts * head_dim * sizeof(float) + parts * sizeof(float);
+}
+
+int tc_decode_partial(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                      const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
+                      int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
+                      int num_splits, float* o_part_dev, float* lse_part_dev, void* stream) {
+  clear_error();
+  int rc = check_common(batch, kv_heads, group, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (n_tokens == 0 && num_splits == 0) return TC_OK;  // empty caches: nothing to read
+  if (!q_dev || !k_dev || !v_dev || !o_part_dev || !lse_part_dev)
+    return fail(TC_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (!aligned16(q_dev) || !aligned16(k_dev) || !aligned16(v_dev) || !aligned16(o_part_dev))
+    return fail(TC_ERR_ALIGNMENT, "q/k/v/o_part base pointers must be 16-byte aligned");
+  if ((rc = check_strides("q", q_strides, 3)) != TC_OK) return rc;
+  if ((rc = check_strides("k", k_strides, 3)) != TC_OK) return rc;
+  if ((rc = check_strides("v", v_strides, 3)) != TC_OK) return rc;
+  if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
+  if (split_tokens <= 0 || split_tokens % kSplitGranule != 0)
+    return fail(TC_ERR_INVALID_ARGUMENT, "split_tokens %d must be a positive multiple of %d", split_tokens,
+                kSplitGranule);
+  if (num_splits < 0 || num_splits > TC_MAX_SPLITS)
+    return fail(TC_ERR_INVALID_ARGUMENT, "num_splits %d outside [0, %d]", num_splits, TC_MAX_SPLITS);
+  if (static_cast<int64_t>(num_splits) * split_tokens < n_tokens)
+    return fail(TC_ERR_INVALID_ARGUMENT, "%d splits of %d tokens do not cover %lld tokens", num_splits, split_tokens,
+                (long long)n_tokens);
+  if (num_splits == 0) return TC_OK;
+  if (!isfinite(scale)) return fail(TC_ERR_INVALID_ARGUMENT, "scale is not finite");
+  // Per-lane buffer offsets span 16 token rows in 32 bits.
+  constexpr int64_t kMaxTokenStride = int64_t(1) << 26;
+  if (k_strides[2] < head_dim || v_strides[2] < head_dim || k_strides[2] >= kMaxTokenStride ||
+      v_strides[2] >= kMaxTokenStride)
+    return fail(TC_ERR_INVALID_ARGUMENT, "k/v token strides (%lld, %lld) outside [%d, 2^26)",
+                (long long)k_strides[2], (long long)v_strides[2], head_dim);
+
+  PartialArgs a;
+  a.q = static_cast<const uint16_t*>(q_dev);
+  a.k = static_cast<const uint16_t*>(k_dev);
+  a.v = static_cast<const uint16_t*>(v_dev);
+  a.o_part = o_part_dev;
+  a.lse_part = lse_part_dev;
+  a.lens = lens_dev;
+  a.n = n_tokens;
+  a.sq_b = q_strides[0]; a.sq_h = q_strides[1]; a.sq_g = q_strides[2];
+  a.sk_b = k_strides[0]; a.sk_h = k_strides[1]; a.sk_t = k_strides[2];
+  a.sv_b = v_strides[0]; a.sv_h = v_strides[1]; a.sv_t = v_strides[2];
+  a.heads = kv_heads;
+  a.group = group;
+  a.splits = num_splits;
+  a.split_tokens = split_tokens;
+  a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, s)
+                                             : launch_partial_dt<TC_DTYPE_BF16>(a, batch, s);
+  return hip_status(e, "decode_partial launch");
+}
+
+int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int batch, int kv_heads, int group,
+                      int head_dim, int num_splits, void* out_dev, const int64_t out_strides[3], int dtype,
+                      void* stream) {
+  clear_error();
+  int rc = check_common(batch, kv_heads, group, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (!out_dev || (num_splits > 0 && (!o_part_dev || !lse_part_dev)))
+    return fail(TC_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (!aligned16(out_dev) || (num_splits > 0 && !aligned16(o_part_dev)))
+    return fail(TC_ERR_ALIGNMENT, "out/o_part base pointers must be 16-byte aligned");
+  if ((rc = check_strides("out", out_strides, 3)) != TC_OK) return rc;
+  if (num_splits < 0 || num_splits > TC_MAX_SPLITS)
+    return fail(TC_ERR_INVALID_ARGUMENT, "num_splits %d outside [0, %d]", num_splits, TC_MAX_SPLITS);
+
+  CombineArgs a;
+  a.o_part = o_part_dev;
+  a.lse_part = lse_part_dev;
+  a.out = static_cast<uint16_t*>(out_dev);
+  a.so_b = out_strides[0]; a.so_h = out_strides[1]; a.so_g = out_strides[2];
+  a.heads = kv_heads;
+  a.group = group;
+  a.splits = num_splits;
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(batch) * kv_heads * group));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TC_DTYPE_F16)
+    hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_F16>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_BF16>), grid, dim3(256), 0, s, a);
+  return hip_status(hipGetLastError(), "decode_combine launch");
+}
+
+int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                        const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
+                        int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
+                        void* workspace_dev, size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
+                        void* stream) {
+  clear_error();
+  int rc = check_common(batch, kv_heads, group, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
+  int t = 0;
+  if ((rc = split_tokens_impl(batch, kv_heads, n_tokens, split_tokens, &t)) != TC_OK) return rc;
+  const int S = static_cast<int>(ceil_div(n_tokens, t));
+  const size_t need = tc_decode_workspace_bytes(batch, kv_heads, group, head_dim, S);
+  if (S > 0 && (!workspace_dev || workspace_bytes < need))
+    return fail(TC_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, need, S);
+  float* o_part = static_cast<float*>(workspace_dev);
+  float* lse_part = S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * group * head_dim : nullptr;
+  if (S > 0) {
+    rc = tc_decode_partial(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch,
+                           kv_heads, group, head_dim, dtype, scale, t, S, o_part, lse_part, stream);
+    if (rc != TC_OK) return rc;
+  }
+  return tc_decode_combine(o_part, lse_part, batch, kv_heads, group, head_dim, S, out_dev, out_strides, dtype, stream);
+}
+
+}  // extern "C"

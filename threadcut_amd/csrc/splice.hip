@@ -1,0 +1,271 @@
+// RoPE delta-shift of post-RoPE keys and the suffix splice of a KV cache.
+//
+// Reference semantics: threadcut/kv.py:15-25 (rotate_half and shift_keys:
+// fp32 math, out = k*cos(emb) + rotate_half(k)*sin(emb), cast back) and
+// :28-41, :83-92 (splice: K[a:a+c] <- shift(K[c0:c0+c], -gap), V[a:a+c] <-
+// V[c0:c0+c], read before written; index_select variant for plain layers).
+//
+// One launch moves every (layer, K|V, batch row, head) strip of the cache.
+// A thread owns one 16-byte chunk of the lower half of a row (dims 8u..8u+7)
+// and the matching chunk of the upper half (64+8u..), which is exactly the
+// pair rotate_half mixes, so each K row is gathered, rotated in fp32 and
+// stored with no intermediate buffer; V rows take the same path unrotated.
+// 8 threads cover a row, a pass of 256 threads covers 32 rows, and a thread
+// keeps kUnroll passes of loads in flight before it stores.
+#include "tc_common.hpp"
+
+namespace tc {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kHalf = kHeadDim / 2;
+constexpr int kThreads = 256;
+constexpr int kRowsPerPass = kThreads / 8;
+constexpr int kUnroll = 4;
+constexpr int kTileRows = kRowsPerPass * kUnroll;  // rows per work-group tile
+constexpr int kMaxJobs = 128;                      // strips sets per launch (64 layers x K,V)
+
+struct SpliceArgs {
+  const uint16_t* src[kMaxJobs];
+  uint16_t* dst[kMaxJobs];
+  float cs[kHeadDim];  // cos(angle_i) for i < 64, then sin(angle_i)
+  int64_t ss_b, ss_h, ss_t;
+  int64_t ds_b, ds_h, ds_t;
+  int64_t src_row0, dst_row0, rows;
+  int heads;
+  int rot_jobs;    // jobs [0, rot_jobs) are keys (rotated), the rest copied
+  int sequential;  // 1: one work-group walks a whole strip in row order
+};
+
+// out = fp(fl(x*cos) + fl(rotate_half(x)*sin)) per element, no contraction:
+// lower half  y = x_lo*cos - x_hi*sin,  upper half y = x_hi*cos + x_lo*sin.
+template <int DT>
+__device__ __forceinline__ void rotate_pair(uint4& lo, uint4& hi, const float (&cv)[8], const float (&sv)[8]) {
+#pragma clang fp contract(off)
+  using E = Elem<DT>;
+  uint32_t wl[4] = {lo.x, lo.y, lo.z, lo.w};
+  uint32_t wh[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float c0 = cv[2 * w], c1 = cv[2 * w + 1];
+    const float s0 = sv[2 * w], s1 = sv[2 * w + 1];
+    const float xl0 = E::lo(wl[w]), xl1 = E::hi(wl[w]);
+    const float xh0 = E::lo(wh[w]), xh1 = E::hi(wh[w]);
+    const float yl0 = xl0 * c0 - xh0 * s0;
+    const float yl1 = xl1 * c1 - xh1 * s1;
+    const float yh0 = xh0 * c0 + xl0 * s0;
+    const float yh1 = xh1 * c1 + xl1 * s1;
+    wl[w] = E::bits(yl0) | (E::bits(yl1) << 16);
+    wh[w] = E::bits(yh0) | (E::bits(yh1) << 16);
+  }
+  lo = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+  hi = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
+  const int job = blockIdx.z;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.heads;
+  const int64_t h = bh % a.heads;
+  const bool rot = job < a.rot_jobs;
+  const int r_in = threadIdx.x >> 3;  // row inside a pass
+  const int u = threadIdx.x & 7;      // 16-byte chunk of each half row
+
+  const uint16_t* src = a.src[job] + b * a.ss_b + h * a.ss_h + 8 * u;
+  uint16_t* dst = a.dst[job] + b * a.ds_b + h * a.ds_h + 8 * u;
+
+  // cos/sin of the thread's 8 frequency pairs (dims 8u..8u+7 and 64+8u..).
+  float cv[8], sv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cv[i] = a.cs[8 * u + i];
+    sv[i] = a.cs[kHalf + 8 * u + i];
+  }
+
+  int64_t row = a.sequential ? 0 : static_cast<int64_t>(blockIdx.x) * kTileRows;
+  const int64_t row_end = a.sequential ? a.rows : min(row + kTileRows, a.rows);
+  for (; row < row_end; row += kTileRows) {
+    uint4 lo[kUnroll], hi[kUnroll];
+#pragma unroll
+    for (int i = 0; i < kUnroll; ++i) {
+      const int64_t r = row + i * kRowsPerPass + r_in;
+      if (r < row_end) {
+        const uint16_t* p = src + (a.src_row0 + r) * a.ss_t;
+        lo[i] = *reinterpret_cast<const uint4*>(p);
+        hi[i] = *reinterpret_cast<const uint4*>(p + kHalf);
+      }
+    }
+    if (a.sequential) {
+      // Sources of this tile may be destinations of the same tile (gap < tile)
+      // and of the next one: every load of the tile lands before any store.
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kUnroll; ++i) {
+      const int64_t r = row + i * kRowsPerPass + r_in;
+      if (r < row_end) {
+        if (rot) rotate_pair<DT>(lo[i], hi[i], cv, sv);
+        uint16_t* p = dst + (a.dst_row0 + r) * a.ds_t;
+        *reinterpret_cast<uint4*>(p) = lo[i];
+        *reinterpret_cast<uint4*>(p + kHalf) = hi[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+
+int check_dims(int batch, int heads, int head_dim, int dtype) {
+  if (batch < 1 || heads < 1 || static_cast<int64_t>(batch) * heads > 65535)
+    return fail(TC_ERR_INVALID_ARGUMENT, "batch %d x heads %d outside [1, 65535]", batch, heads);
+  if (head_dim != kHeadDim) return fail(TC_ERR_UNSUPPORTED, "head_dim %d unsupported (kernels are built for 128)", head_dim);
+  if (dtype != TC_DTYPE_F16 && dtype != TC_DTYPE_BF16) return fail(TC_ERR_UNSUPPORTED, "dtype %d unsupported", dtype);
+  return TC_OK;
+}
+
+int check_strides3(const char* what, const int64_t* st) {
+  if (!st) return fail(TC_ERR_INVALID_ARGUMENT, "%s strides are null", what);
+  for (int i = 0; i < 3; ++i) {
+    if (st[i] < 0) return fail(TC_ERR_INVALID_ARGUMENT, "%s stride %d is negative", what, i);
+    if (st[i] % 8) return fail(TC_ERR_ALIGNMENT, "%s stride %d (%lld) not a multiple of 8", what, i, (long long)st[i]);
+  }
+  if (st[2] < kHeadDim) return fail(TC_ERR_INVALID_ARGUMENT, "%s token stride %lld overlaps rows", what, (long long)st[2]);
+  return TC_OK;
+}
+
+int check_ptrs(const char* what, void* const* ptrs, int n) {
+  if (n > 0 && !ptrs) return fail(TC_ERR_INVALID_ARGUMENT, "%s pointer array is null", what);
+  for (int i = 0; i < n; ++i) {
+    if (!ptrs[i]) return fail(TC_ERR_INVALID_ARGUMENT, "%s[%d] is null", what, i);
+    if (!aligned16(ptrs[i])) return fail(TC_ERR_ALIGNMENT, "%s[%d] is not 16-byte aligned", what, i);
+  }
+  return TC_OK;
+}
+
+// Launches the kernel over `layers` layers, K strips rotated when `rotate`;
+// vsrc == nullptr moves keys only.
+int launch_rows(void* const* ksrc, void* const* vsrc, void* const* kdst, void* const* vdst, int layers,
+                const int64_t* ss, const int64_t* ds, int batch, int heads, int dtype, int64_t src_row0,
+                int64_t dst_row0, int64_t rows, bool rotate, bool sequential, const float* cos_sin,
+                hipStream_t stream) {
+  if (rows <= 0 || layers <= 0) return TC_OK;
+  constexpr int kLayersPerLaunch = kMaxJobs / 2;
+  const int per_layer = vsrc ? 2 : 1;
+  for (int l0 = 0; l0 < layers; l0 += kLayersPerLaunch) {
+    const int nl = min(kLayersPerLaunch, layers - l0);
+    SpliceArgs a;
+    for (int i = 0; i < nl; ++i) {
+      a.src[i] = static_cast<const uint16_t*>(ksrc[l0 + i]);
+      a.dst[i] = static_cast<uint16_t*>(kdst[l0 + i]);
+      if (vsrc) {
+        a.src[nl + i] = static_cast<const uint16_t*>(vsrc[l0 + i]);
+        a.dst[nl + i] = static_cast<uint16_t*>(vdst[l0 + i]);
+      }
+    }
+    for (int i = per_layer * nl; i < kMaxJobs; ++i) { a.src[i] = nullptr; a.dst[i] = nullptr; }
+    for (int i = 0; i < kHeadDim; ++i) a.cs[i] = (rotate && cos_sin) ? cos_sin[i] : 0.f;
+    a.ss_b = ss[0]; a.ss_h = ss[1]; a.ss_t = ss[2];
+    a.ds_b = ds[0]; a.ds_h = ds[1]; a.ds_t = ds[2];
+    a.src_row0 = src_row0;
+    a.dst_row0 = dst_row0;
+    a.rows = rows;
+    a.heads = heads;
+    a.rot_jobs = rotate ? nl : 0;
+    a.sequential = sequential ? 1 : 0;
+    const int64_t tiles = sequential ? 1 : ceil_div(rows, kTileRows);
+    if (tiles > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many rows (%lld)", (long long)rows);
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batch * heads),
+                    static_cast<unsigned>(per_layer * nl));
+    if (dtype == TC_DTYPE_F16)
+      hipLaunchKernelGGL((splice_kernel<TC_DTYPE_F16>), grid, dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((splice_kernel<TC_DTYPE_BF16>), grid, dim3(kThreads), 0, stream, a);
+    const int rc = hip_status(hipGetLastError(), "splice launch");
+    if (rc != TC_OK) return rc;
+  }
+  return TC_OK;
+}
+
+}  // namespace
+}  // namespace tc
+
+using namespace tc;
+
+extern "C" {
+
+int tc_shift_keys(const void* keys_dev, const int64_t src_strides[3], void* out_dev, const int64_t dst_strides[3],
+                  int batch, int heads, int64_t tokens, int head_dim, int dtype, const float* cos_sin_host,
+                  void* stream) {
+  clear_error();
+  int rc = check_dims(batch, heads, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if ((rc = check_strides3("keys", src_strides)) != TC_OK) return rc;
+  if ((rc = check_strides3("out", dst_strides)) != TC_OK) return rc;
+  if (tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "tokens %lld is negative", (long long)tokens);
+  if (tokens == 0) return TC_OK;
+  if (!keys_dev || !out_dev || !cos_sin_host) return fail(TC_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!aligned16(keys_dev) || !aligned16(out_dev)) return fail(TC_ERR_ALIGNMENT, "keys/out not 16-byte aligned");
+  if (keys_dev == out_dev) return fail(TC_ERR_INVALID_ARGUMENT, "out may not alias keys");
+  void* k = const_cast<void*>(keys_dev);
+  void* o = out_dev;
+  return launch_rows(&k, nullptr, &o, nullptr, 1, src_strides, dst_strides, batch, heads, dtype, 0, 0, tokens, true,
+                     false, cos_sin_host, static_cast<hipStream_t>(stream));
+}
+
+int tc_splice_rope(void* const* k_layers_host, void* const* v_layers_host, int num_layers, const int64_t strides[3],
+                   int batch, int heads, int64_t capacity, int head_dim, int dtype, int64_t a, int64_t c0, int64_t c,
+                   const float* cos_sin_host, void* stream) {
+  clear_error();
+  int rc = check_dims(batch, heads, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (num_layers < 0) return fail(TC_ERR_INVALID_ARGUMENT, "num_layers %d is negative", num_layers);
+  if ((rc = check_strides3("cache", strides)) != TC_OK) return rc;
+  if (a < 0 || c < 0 || c0 < a)
+    return fail(TC_ERR_INVALID_ARGUMENT, "split (a=%lld, c0=%lld, c=%lld) needs 0 <= a <= c0 and c >= 0", (long long)a,
+                (long long)c0, (long long)c);
+  if (c0 + c > capacity)
+    return fail(TC_ERR_INVALID_ARGUMENT, "suffix [%lld, %lld) past the capacity %lld", (long long)c0,
+                (long long)(c0 + c), (long long)capacity);
+  if ((rc = check_ptrs("k_layers", k_layers_host, num_layers)) != TC_OK) return rc;
+  if ((rc = check_ptrs("v_layers", v_layers_host, num_layers)) != TC_OK) return rc;
+  if (c == 0 || c0 == a || num_layers == 0) return TC_OK;
+  if (!cos_sin_host) return fail(TC_ERR_INVALID_ARGUMENT, "cos_sin table is null");
+  const bool overlap = (c0 - a) < c;
+  return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides, batch,
+                     heads, dtype, c0, a, c, true, overlap, cos_sin_host, static_cast<hipStream_t>(stream));
+}
+
+int tc_splice_copy(void* const* k_src_host, void* const* v_src_host, const int64_t src_strides[3], int64_t src_tokens,
+                   void* const* k_dst_host, void* const* v_dst_host, const int64_t dst_strides[3], int num_layers,
+                   int batch, int heads, int head_dim, int dtype, int64_t a, int64_t c0, int64_t c,
+                   const float* cos_sin_host, void* stream) {
+  clear_error();
+  int rc = check_dims(batch, heads, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (num_layers < 0) return fail(TC_ERR_INVALID_ARGUMENT, "num_layers %d is negative", num_layers);
+  if ((rc = check_strides3("src", src_strides)) != TC_OK) return rc;
+  if ((rc = check_strides3("dst", dst_strides)) != TC_OK) return rc;
+  if (a < 0 || c < 0 || c0 < a)
+    return fail(TC_ERR_INVALID_ARGUMENT, "split (a=%lld, c0=%lld, c=%lld) needs 0 <= a <= c0 and c >= 0", (long long)a,
+                (long long)c0, (long long)c);
+  if (c0 + c > src_tokens || a > src_tokens)
+    return fail(TC_ERR_INVALID_ARGUMENT, "split past the %lld source tokens", (long long)src_tokens);
+  if ((rc = check_ptrs("k_src", k_src_host, num_layers)) != TC_OK) return rc;
+  if ((rc = check_ptrs("v_src", v_src_host, num_layers)) != TC_OK) return rc;
+  if ((rc = check_ptrs("k_dst", k_dst_host, num_layers)) != TC_OK) return rc;
+  if ((rc = check_ptrs("v_dst", v_dst_host, num_layers)) != TC_OK) return rc;
+  const bool rotate = c > 0 && c0 != a;
+  if (rotate && !cos_sin_host) return fail(TC_ERR_INVALID_ARGUMENT, "cos_sin table is null");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch_rows(k_src_host, v_src_host, k_dst_host, v_dst_host, num_layers, src_strides, dst_strides, batch, heads,
+                   dtype, 0, 0, a, false, false, nullptr, s);
+  if (rc != TC_OK) return rc;
+  return launch_rows(k_src_host, v_src_host, k_dst_host, v_dst_host, num_layers, src_strides, dst_strides, batch,
+                     heads, dtype, c0, a, c, rotate, false, cos_sin_host, s);
+}
+
+}  // extern "C"

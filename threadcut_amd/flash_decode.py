@@ -1,0 +1,159 @@
+"""Split-KV GQA decode attention (flash-decoding) on MI355X.
+
+Drop-in for threadcut/flash_decode.py:57-69 (``decode_attention``). One decode
+step has a single query token, so each KV head serves only g = Hq/Hkv query
+rows. The partial kernel gives every (split, KV head, sequence) its own
+256-thread work-group, streams that slice of K/V once from HBM with the g
+query rows held in registers, and writes a partial output plus its
+log-sum-exp; a second kernel merges the splits with softmax(lse) weights
+(threadcut/flash_decode.py:68-69). Both are HIP kernels of
+``libthreadcut_hip.so``; this module only checks tensors and passes pointers,
+strides and the current stream.
+"""
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+SPLIT_GRANULE = 64  # tokens; split lengths are rounded up to this
+
+
+def num_splits(batch, kv_heads, n_tokens, split=None):
+    """KV splits a call of this size uses (``split=None``: tuned to fill the GPU)."""
+    lib = _lib.load()
+    s = lib.tc_decode_num_splits(int(batch), int(kv_heads), int(n_tokens), int(split or 0))
+    if s < 0:
+        _lib.check(-s, "tc_decode_num_splits")
+    return s
+
+
+def split_tokens(batch, kv_heads, n_tokens, split=None):
+    """Tokens per split a call of this size uses."""
+    lib = _lib.load()
+    t = lib.tc_decode_split_tokens(int(batch), int(kv_heads), int(n_tokens), int(split or 0))
+    if t < 0:
+        _lib.check(-t, "tc_decode_split_tokens")
+    return t
+
+
+def _check_qkv(q, k, v, what):
+    _lib.require_gpu(q, k, v, what=what)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError(f"{what}: expected q [B,Hkv,G,D], k/v [B,Hkv,N,D]")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"{what}: q/k/v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"{what}: q/k/v on different devices")
+    b, hkv, g, d = q.shape
+    if k.shape[:2] != (b, hkv) or v.shape[:2] != (b, hkv) or k.shape[3] != d or v.shape[3] != d:
+        raise ValueError(f"{what}: shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} disagree")
+    if v.shape[2] != k.shape[2]:
+        raise ValueError(f"{what}: k and v hold {k.shape[2]} and {v.shape[2]} tokens")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.stride(3) != 1:
+            raise ValueError(f"{what}: {name} must have a contiguous last dimension")
+
+
+def _strides3(t, token_dim=False):
+    """Element strides of dims 0-2; size-1 dims get a harmless canonical stride."""
+    st = [t.stride(i) if t.shape[i] > 1 else 0 for i in range(3)]
+    if token_dim and t.shape[2] <= 1:
+        st[2] = t.shape[3]
+    return _lib.i64x3(*st)
+
+
+def decode_into(q, k, v, scale, out, lens=None, split=None):
+    """out[b,h,g,:] = softmax(q[b,h,g]·k[b,h,:len_b]ᵀ·scale)·v[b,h,:len_b] (fp32 math).
+
+    q [B,Hkv,G,D], k/v [B,Hkv,N,D] (any strides, last dim contiguous), out
+    [B,Hkv,G,D] in q.dtype, lens optional int32 [B] on the device (every
+    lens[b] <= N; without lens all N tokens are used). Enqueued on the
+    current stream; returns out.
+    """
+    _check_qkv(q, k, v, "decode_attention")
+    b, hkv, g, d = q.shape
+    n = k.shape[2]
+    if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or out.stride(3) != 1:
+        raise ValueError("decode_attention: out must match q in shape, dtype and device")
+    if lens is not None:
+        if lens.dtype != torch.int32 or lens.device != q.device or lens.shape != (b,) or not lens.is_contiguous():
+            raise ValueError("decode_attention: lens must be a contiguous int32 [B] tensor on the device")
+    lib = _lib.load()
+    dt = _lib.dtype_code(q.dtype)
+    with torch.cuda.device(q.device):
+        s = num_splits(b, hkv, n, split)
+        nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+        rc = lib.tc_decode_attention(
+            q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k, True), v.data_ptr(), _strides3(v, True),
+            lens.data_ptr() if lens is not None else None, n,
+            b, hkv, g, d, dt, float(scale), int(split or 0),
+            ws.data_ptr(), ws.numel(), out.data_ptr(), _strides3(out), _lib.stream_of(q.device))
+        _lib.check(rc, "tc_decode_attention")
+    return out
+
+
+def decode_attention_batched(q, k, v, scale, lens=None, split=None):
+    """Batched form: q [B,Hkv,G,D], k/v [B,Hkv,N,D] → [B,Hkv,G,D] in q.dtype."""
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    return decode_into(q, k, v, scale, out, lens=lens, split=split)
+
+
+def decode_attention(q, k, v, scale, split=None, block=16):
+    """q: [hkv, g, d]; k, v: [hkv, n, d] (last dim contiguous). Returns [hkv, g, d].
+
+    Signature of threadcut/flash_decode.py:57. ``split`` is the number of
+    tokens per KV split (rounded up to 64); None tunes it so the work-groups
+    fill the GPU. ``block`` is accepted for compatibility: the kernel's
+    token block is fixed at 16 per wave.
+    """
+    del block
+    return decode_attention_batched(q[None], k[None], v[None], scale, split=split)[0]
+
+
+class DecodePlan:
+    """A decode call with fixed tensors, prepared once and launched many times.
+
+    Holds the ctypes arguments and a workspace, so ``run()`` is one library
+    call with no allocation (usable inside HIP graph capture). The tensors
+    must stay alive and keep their storage while the plan is used.
+    """
+
+    def __init__(self, q, k, v, scale, out, lens=None, split=None):
+        _check_qkv(q, k, v, "DecodePlan")
+        b, hkv, g, d = q.shape
+        self.lib = _lib.load()
+        self.device = q.device
+        with torch.cuda.device(q.device):
+            self.splits = num_splits(b, hkv, k.shape[2], split)
+            self.split_tokens = split_tokens(b, hkv, k.shape[2], split)
+            nbytes = self.lib.tc_decode_workspace_bytes(b, hkv, g, d, self.splits)
+            self.workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+        self.tensors = (q, k, v, out, lens)
+        self.args = (q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k, True), v.data_ptr(),
+                     _strides3(v, True), lens.data_ptr() if lens is not None else None, k.shape[2],
+                     b, hkv, g, d, _lib.dtype_code(q.dtype), float(scale), self.split_tokens,
+                     self.workspace.data_ptr(), self.workspace.numel(), out.data_ptr(), _strides3(out))
+        n = k.shape[2]
+        parts = b * hkv * self.splits * g
+        self.o_part = self.workspace.data_ptr()
+        self.lse_part = self.o_part + parts * d * 4
+        self.partial_args = (q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k, True), v.data_ptr(),
+                             _strides3(v, True), lens.data_ptr() if lens is not None else None, n,
+                             b, hkv, g, d, _lib.dtype_code(q.dtype), float(scale), self.split_tokens,
+                             self.splits, self.o_part, self.lse_part)
+        self.combine_args = (self.o_part, self.lse_part, b, hkv, g, d, self.splits, out.data_ptr(),
+                             _strides3(out), _lib.dtype_code(q.dtype))
+
+    def run(self, stream=None):
+        """Both kernels on `stream` (default: the current stream)."""
+        s = stream if stream is not None else _lib.stream_of(self.device)
+        _lib.check(self.lib.tc_decode_attention(*self.args, s), "tc_decode_attention")
+
+    def run_partial(self, stream=None):
+        s = stream if stream is not None else _lib.stream_of(self.device)
+        _lib.check(self.lib.tc_decode_partial(*self.partial_args, s), "tc_decode_partial")
+
+    def run_combine(self, stream=None):
+        s = stream if stream is not None else _lib.stream_of(self.device)
+        _lib.check(self.lib.tc_decode_combine(*self.combine_args, s), "tc_decode_combine")

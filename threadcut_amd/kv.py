@@ -1,0 +1,207 @@
+"""KV cache surgery on MI355X: drop a pruned span B and move C left, keys re-rotated.
+
+Drop-in for threadcut/kv.py:15-98. Keys are cached after RoPE and rotations
+compose, so rotating a key stored at position p by -gap gives the key at
+p - gap; values carry no position and move unchanged. The per-layer torch op
+chains of the reference (about eight kernels and fp32 temporaries per layer,
+36 layers) become one HIP launch (``tc_splice_rope``) that gathers, rotates
+and stores every layer's suffix in place.
+
+The rotation table cos/sin(delta * inv_freq) is built on the host with the
+reference's own op order (threadcut/kv.py:22-23) and passed by value in the
+kernel arguments; the kernel then evaluates fl(k*cos) + fl(rotate_half(k)*sin)
+without contraction, so shifted keys match the reference's fp32 op sequence
+bit for bit.
+"""
+import torch
+from transformers import DynamicCache
+from transformers.cache_utils import DynamicLayer
+
+from . import _lib
+from .match import Split  # noqa: F401  (re-exported: the splice contract)
+
+HEAD_DIM = 128
+
+
+def rotate_half(x):
+    """cat(-x2, x1) over the two halves of the last dim (threadcut/kv.py:15-17)."""
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def rope_table(delta, inv_freq):
+    """Host fp32 [D] = cos(angle) ++ sin(angle), angle = delta * inv_freq.
+
+    Same op sequence as threadcut/kv.py:22-23 (`delta * inv_freq.float()`,
+    emb = cat(angle, angle), emb.cos(), emb.sin()), evaluated on the host CPU;
+    emb's upper half repeats the lower one, so only the lower half is kept.
+    """
+    f = inv_freq.detach().to("cpu").float()
+    angle = delta * f
+    emb = torch.cat((angle, angle))
+    half = f.numel()
+    return torch.cat((emb.cos()[:half], emb.sin()[:half]))
+
+
+def _as4(t):
+    if t.dim() == 4:
+        return t
+    if t.dim() == 3:
+        return t.unsqueeze(0)
+    if t.dim() == 2:
+        return t.unsqueeze(0).unsqueeze(0)
+    raise ValueError(f"expected a [..., tokens, head_dim] tensor of rank 2-4, got {tuple(t.shape)}")
+
+
+def shift_keys(keys, delta, inv_freq):
+    """Move post-RoPE keys by `delta` positions (negative = left); new tensor.
+
+    threadcut/kv.py:20-25: fp32 math, result in keys.dtype. keys is any
+    [..., tokens, 128] fp16/bf16 GPU tensor with a contiguous last dim.
+    """
+    _lib.require_gpu(keys, what="shift_keys")
+    k4 = _as4(keys)
+    b, h, t, d = k4.shape
+    if d != HEAD_DIM:
+        raise ValueError(f"shift_keys: head_dim {d} unsupported (128)")
+    if k4.stride(3) != 1:
+        raise ValueError("shift_keys: keys must have a contiguous last dimension")
+    out = torch.empty(keys.shape, dtype=keys.dtype, device=keys.device)
+    o4 = _as4(out)
+    table = _lib.float_array(rope_table(delta, inv_freq))
+    lib = _lib.load()
+    with torch.cuda.device(keys.device):
+        rc = lib.tc_shift_keys(k4.data_ptr(), _lib.i64x3(k4.stride(0), k4.stride(1), k4.stride(2)),
+                               o4.data_ptr(), _lib.i64x3(o4.stride(0), o4.stride(1), o4.stride(2)),
+                               b, h, t, d, _lib.dtype_code(keys.dtype), table, _lib.stream_of(keys.device))
+    _lib.check(rc, "tc_shift_keys")
+    return out
+
+
+def _splice_buffers(kbufs, vbufs, s, inv_freq):
+    """In-place A·B·C -> A·C over equally shaped [B, H, cap, 128] buffers."""
+    k0 = kbufs[0]
+    b, h, cap, d = k0.shape
+    for t in (*kbufs, *vbufs):
+        if t.shape != k0.shape or t.stride() != k0.stride() or t.dtype != k0.dtype or t.device != k0.device:
+            raise ValueError("splice: every layer's K/V buffer must share shape, strides, dtype and device")
+    _lib.require_gpu(k0, what="splice")
+    table = _lib.float_array(rope_table(-s.gap, inv_freq)) if s.c and s.gap else None
+    lib = _lib.load()
+    with torch.cuda.device(k0.device):
+        rc = lib.tc_splice_rope(_lib.ptr_array([t.data_ptr() for t in kbufs]),
+                                _lib.ptr_array([t.data_ptr() for t in vbufs]), len(kbufs),
+                                _lib.i64x3(k0.stride(0), k0.stride(1), k0.stride(2)), b, h, cap, d,
+                                _lib.dtype_code(k0.dtype), s.a, s.c0, s.c, table, _lib.stream_of(k0.device))
+    _lib.check(rc, "tc_splice_rope")
+
+
+def _group_by_layout(layers):
+    groups = {}
+    for layer in layers:
+        t = layer.kbuf
+        key = (tuple(t.shape), t.stride(), t.dtype, t.device)
+        groups.setdefault(key, []).append(layer)
+    return groups.values()
+
+
+def splice(cache, s, inv_freq):
+    """Rewrite every layer of a DynamicCache from A·B·C·(tail) to A·C (threadcut/kv.py:28-41)."""
+    if all(isinstance(layer, GrowingLayer) for layer in cache.layers):
+        live = [layer for layer in cache.layers if getattr(layer, "kbuf", None) is not None]
+        for layer in live:
+            if s.c0 + s.c > layer.n:
+                raise ValueError(f"splice: suffix [{s.c0}, {s.c0 + s.c}) past the {layer.n} cached tokens")
+        if s.c and s.gap:
+            for group in _group_by_layout(live):
+                _splice_buffers([l.kbuf for l in group], [l.vbuf for l in group], s, inv_freq)
+        for layer in live:
+            layer.n = s.a + s.c
+            layer._view()
+        return
+    layers = cache.layers
+    k0 = layers[0].keys
+    _lib.require_gpu(k0, what="splice")
+    b, h, n, d = k0.shape
+    if s.c0 + s.c > n or s.a > n:
+        raise ValueError(f"splice: split {s} past the {n} cached tokens")
+    new_k = [torch.empty((b, h, s.a + s.c, d), dtype=k0.dtype, device=k0.device) for _ in layers]
+    new_v = [torch.empty_like(t) for t in new_k]
+    for layer in layers:
+        for t in (layer.keys, layer.values):
+            if t.shape != k0.shape or t.stride() != k0.stride() or t.dtype != k0.dtype:
+                raise ValueError("splice: every layer's keys/values must share shape, strides and dtype")
+    table = _lib.float_array(rope_table(-s.gap, inv_freq)) if s.c and s.gap else None
+    src_st = _lib.i64x3(k0.stride(0), k0.stride(1), k0.stride(2))
+    t0 = new_k[0]
+    dst_st = _lib.i64x3(t0.stride(0), t0.stride(1), t0.stride(2))
+    lib = _lib.load()
+    with torch.cuda.device(k0.device):
+        rc = lib.tc_splice_copy(_lib.ptr_array([l.keys.data_ptr() for l in layers]),
+                                _lib.ptr_array([l.values.data_ptr() for l in layers]), src_st, n,
+                                _lib.ptr_array([t.data_ptr() for t in new_k]),
+                                _lib.ptr_array([t.data_ptr() for t in new_v]), dst_st, len(layers),
+                                b, h, d, _lib.dtype_code(k0.dtype), s.a, s.c0, s.c, table,
+                                _lib.stream_of(k0.device))
+    _lib.check(rc, "tc_splice_copy")
+    for layer, k, v in zip(layers, new_k, new_v):
+        layer.keys, layer.values = k, v
+
+
+class GrowingLayer(DynamicLayer):
+    """DynamicLayer backed by a preallocated buffer (threadcut/kv.py:44-92).
+
+    Appending a token writes in place instead of re-copying the cache with
+    torch.cat. Capacity grows by max(need, 1.25 * cap, cap + 2048) tokens.
+    ``keys``/``values`` are views ``kbuf[..., :n, :]``.
+    """
+
+    def lazy_initialization(self, key_states, value_states):
+        super().lazy_initialization(key_states, value_states)
+        self.n, self.kbuf, self.vbuf = 0, None, None
+
+    def _reserve(self, need, like):
+        cap = 0 if self.kbuf is None else self.kbuf.shape[-2]
+        if need <= cap:
+            return
+        new = max(need, int(cap * 1.25), cap + 2048)
+        kb = like.new_empty((*like.shape[:-2], new, like.shape[-1]))
+        vb = torch.empty_like(kb)
+        if self.n:
+            kb[..., :self.n, :] = self.kbuf[..., :self.n, :]
+            vb[..., :self.n, :] = self.vbuf[..., :self.n, :]
+        self.kbuf, self.vbuf = kb, vb
+
+    def _view(self):
+        self.keys, self.values = self.kbuf[..., :self.n, :], self.vbuf[..., :self.n, :]
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        add = key_states.shape[-2]
+        self._reserve(self.n + add, key_states)
+        self.kbuf[..., self.n:self.n + add, :] = key_states
+        self.vbuf[..., self.n:self.n + add, :] = value_states
+        self.n += add
+        self._view()
+        return self.keys, self.values
+
+    def crop(self, max_length):
+        self.n = min(self.n, max_length)
+        self._view()
+
+    def splice(self, s, inv_freq):
+        """In-place A·B·C -> A·C: only C is touched, so a prune costs O(|C|)."""
+        if s.c0 + s.c > self.n:
+            raise ValueError(f"splice: suffix [{s.c0}, {s.c0 + s.c}) past the {self.n} cached tokens")
+        if s.c and s.gap:
+            _splice_buffers([self.kbuf], [self.vbuf], s, inv_freq)
+        self.n = s.a + s.c
+        self._view()
+
+
+def new_cache(config):
+    """A DynamicCache whose layers are GrowingLayers (threadcut/kv.py:95-98)."""
+    cache = DynamicCache(config=config)
+    cache.layers = [GrowingLayer() for _ in cache.layers]
+    return cache
