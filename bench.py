@@ -153,8 +153,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-splice", action="store_true")
-    ap.add_argument("--only", choices=["decode", "partial", "splice"], default=None,
-                    help="run one measurement only (for profiling)")
+    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy"], default=None,
+                    help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
+                         "the calibration kernel of the HBM byte counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -173,6 +174,14 @@ def main():
 
     if args.only == "splice":
         print(json.dumps(bench_splice(dev, args.steps, args.warmup)))
+        return
+    if args.only == "copy":
+        src = torch.empty(128 << 20, dtype=torch.float16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 2, "launches": args.warmup + args.steps}))
         return
 
     n = args.n

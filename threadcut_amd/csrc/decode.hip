@@ -28,10 +28,31 @@
 namespace tc {
 namespace {
 
+// Tuning knobs (measured on MI355X; override with -D for sweeps).
+#ifndef TC_DECODE_WAVES
+#define TC_DECODE_WAVES 4   // waves per partial work-group
+#endif
+#ifndef TC_DECODE_DEPTH
+#define TC_DECODE_DEPTH 2   // 16-token tiles in flight per wave
+#endif
+#ifndef TC_DECODE_AUX
+#define TC_DECODE_AUX 2     // cache-policy bits of the K/V buffer loads (2: non-temporal stream)
+#endif
+#ifndef TC_DECODE_PERMLANE
+#define TC_DECODE_PERMLANE 1  // merge the four rows of a wave with v_permlane{16,32}_swap
+#endif
+#ifndef TC_DECODE_INTERLEAVE
+#define TC_DECODE_INTERLEAVE 1  // tc_decode_attention deals tiles round-robin over the splits
+#endif
+#ifndef TC_DECODE_WGS_PER_CU
+#define TC_DECODE_WGS_PER_CU 1  // partial work-groups per compute unit the split heuristic aims at
+#endif
+
 constexpr int kHeadDim = 128;
-constexpr int kWaves = 4;                            // waves per work-group
+constexpr int kWaves = TC_DECODE_WAVES;
+constexpr int kDepth = TC_DECODE_DEPTH;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
-constexpr int kSplitGranule = kWaves * kWaveIter;    // split length granule
+constexpr int kSplitGranule = kWaves * kWaveIter > 64 ? kWaves * kWaveIter : 64;  // split length granule
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -47,6 +68,7 @@ struct PartialArgs {
   int64_t sk_b, sk_h, sk_t;
   int64_t sv_b, sv_h, sv_t;
   int heads, group, splits, split_tokens;
+  int interleave;      // 0: split s owns tokens [s*T, (s+1)*T); 1: 16-token tiles dealt round-robin
   float scale_log2;    // softmax scale * log2(e)
 };
 
@@ -157,6 +179,39 @@ __device__ __forceinline__ float owner_bcast(const float* x, int j, int hh) {
   return row_bcast_dyn(x[owner_reg<GP>(hh)], owner_lane<GP>(j, hh));
 }
 
+// Reductions over the four 16-lane rows of a wave (every lane gets the result).
+#if TC_DECODE_PERMLANE
+// v_permlane16_swap(x, x) leaves rows (x0, x0, x2, x2) and (x1, x1, x3, x3) in its two
+// results, so their sum is x0 + x1 (x2 + x3) in every lane; permlane32 pairs the halves.
+__device__ __forceinline__ float pair16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) { return pair32_sum(pair16_sum(x)); }
+__device__ __forceinline__ float rows_max(float x) { return pair32_max(pair16_max(x)); }
+#else
+__device__ __forceinline__ float rows_sum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+__device__ __forceinline__ float rows_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+#endif
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Buffer resource over `bytes` bytes at p; loads past the end return zero.
@@ -165,7 +220,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int32
 }
 
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int32_t off) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, TC_DECODE_AUX);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -279,10 +334,24 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
 
   // Lengths past the buffer (or negative) are clamped into [0, n].
   const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), a.n) : a.n;
-  const int wave_tokens = a.split_tokens / kWaves;
-  const int64_t start = static_cast<int64_t>(split) * a.split_tokens +
-                        static_cast<int64_t>(wave) * wave_tokens;
-  const int64_t end = min(start + wave_tokens, len);
+  // The wave's 16-token tiles: first, first + stride, ... with tokens < end.
+  // Contiguous: split s, wave w own [s*T + w*T/W, s*T + (w+1)*T/W). Interleaved:
+  // all S*W waves of a head sweep the cache together, wave g taking tiles
+  // g, g + S*W, ..., so the loads in flight at any moment are adjacent in HBM.
+  int64_t first_tile, tile_stride, end;
+  if (a.interleave) {
+    first_tile = static_cast<int64_t>(split) * kWaves + wave;
+    tile_stride = static_cast<int64_t>(a.splits) * kWaves;
+    end = len;
+  } else {
+    const int wave_tokens = a.split_tokens / kWaves;
+    const int64_t start = static_cast<int64_t>(split) * a.split_tokens + static_cast<int64_t>(wave) * wave_tokens;
+    first_tile = start / kWaveIter;
+    tile_stride = 1;
+    end = min(start + wave_tokens, len);
+  }
+  const int64_t first_tok = first_tile * kWaveIter;
+  const int64_t ntiles = end > first_tok ? ceil_div(end - first_tok, kWaveIter * tile_stride) : 0;
 
   // The lane's 8 dims of every query row, in the lane's head order.
   uint32_t qw[GP][4];
@@ -312,16 +381,28 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   st.init();
   const int my_slot = 4 * (c >> 2) + grp;  // token slot of the lane's score(s)
 
-  if (start < end) {
-    Tile t0, t1;
-    load_tile(t0, kslab, vslab, row_k, row_v, start, end, koff, voff);
-    for (int64_t tok = start;; tok += 2 * kWaveIter) {
-      load_tile(t1, kslab, vslab, row_k, row_v, tok + kWaveIter, end, koff, voff);
-      st.step(t0, qw, tok + my_slot < end, a.scale_log2);
-      if (tok + kWaveIter >= end) break;
-      load_tile(t0, kslab, vslab, row_k, row_v, tok + 2 * kWaveIter, end, koff, voff);
-      st.step(t1, qw, tok + kWaveIter + my_slot < end, a.scale_log2);
-      if (tok + 2 * kWaveIter >= end) break;
+  if (ntiles > 0) {
+    // Ring of kDepth tiles: tile d of a round is computed while the next
+    // kDepth - 1 tiles are in flight (indices fold to constants when unrolled).
+    // Loads past `end` read nothing (the buffer range is empty there).
+    const int64_t tok_step = tile_stride * kWaveIter;
+    Tile t[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth - 1; ++d)
+      load_tile(t[d], kslab, vslab, row_k, row_v, first_tok + d * tok_step, end, koff, voff);
+    for (int64_t i = 0;; i += kDepth) {
+      bool done = false;
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        if (!done) {
+          const int64_t tok = first_tok + (i + d) * tok_step;
+          load_tile(t[(d + kDepth - 1) % kDepth], kslab, vslab, row_k, row_v, tok + (kDepth - 1) * tok_step, end,
+                    koff, voff);
+          st.step(t[d], qw, tok + my_slot < end, a.scale_log2);
+          done = i + d + 1 >= ntiles;
+        }
+      }
+      if (done) break;
     }
   }
 
@@ -340,21 +421,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   // Merge the four rows (lanes c, c+16, c+32, c+48 hold the same dims).
 #pragma unroll
   for (int hh = 0; hh < GP; ++hh) {
-    float M = fmaxf(mh[hh], __shfl_xor(mh[hh], 16));
-    M = fmaxf(M, __shfl_xor(M, 32));
+    const float M = rows_max(mh[hh]);
     const float f = __builtin_amdgcn_exp2f(mh[hh] - ((M == neg_inf()) ? 0.f : M));
-    float L = lh[hh] * f;
-    L += __shfl_xor(L, 16);
-    L += __shfl_xor(L, 32);
+    lh[hh] = rows_sum(lh[hh] * f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float y = st.acc[hh][e] * f;
-      y += __shfl_xor(y, 16);
-      y += __shfl_xor(y, 32);
-      st.acc[hh][e] = y;
-    }
+    for (int e = 0; e < 8; ++e) st.acc[hh][e] = rows_sum(st.acc[hh][e] * f);
     mh[hh] = M;
-    lh[hh] = L;
   }
 
   // Merge the waves through LDS and write this split's partial.
@@ -391,78 +463,94 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   }
 }
 
-// One work-group per (sequence, kv head, query head): weights exp(lse - max)
-// over the splits, 8 split lanes x 32 dim quads accumulate o, LDS reduce.
+// Combine: one 256-thread work-group per (sequence, kv head, query head,
+// 32-dim quarter). Thread (sl, dq) folds splits sl, sl + 32, ... of dims
+// 4*dq .. 4*dq+3 with a running (max, sum, weighted o); the 32 split lanes are
+// merged with wave shuffles and one LDS exchange. All loads are issued before
+// any is consumed, so a call costs one memory round trip.
+constexpr int kCombineLanes = 32;   // split lanes per work-group
+constexpr int kCombineQuads = 8;    // float4 dim quads per work-group (32 dims)
+
+struct Acc4 {
+  float m, l;
+  float4 o;
+};
+
+__device__ __forceinline__ Acc4 merge(const Acc4& a, const Acc4& b) {
+  const float M = fmaxf(a.m, b.m);
+  const float Ms = (M == neg_inf()) ? 0.f : M;
+  const float fa = __builtin_amdgcn_exp2f((a.m - Ms) * kLog2e);
+  const float fb = __builtin_amdgcn_exp2f((b.m - Ms) * kLog2e);
+  Acc4 r;
+  r.m = M;
+  r.l = a.l * fa + b.l * fb;
+  r.o = make_float4(a.o.x * fa + b.o.x * fb, a.o.y * fa + b.o.y * fb, a.o.z * fa + b.o.z * fb,
+                    a.o.w * fa + b.o.w * fb);
+  return r;
+}
+
+__device__ __forceinline__ Acc4 shfl_xor(const Acc4& a, int mask) {
+  Acc4 r;
+  r.m = __shfl_xor(a.m, mask);
+  r.l = __shfl_xor(a.l, mask);
+  r.o = make_float4(__shfl_xor(a.o.x, mask), __shfl_xor(a.o.y, mask), __shfl_xor(a.o.z, mask),
+                    __shfl_xor(a.o.w, mask));
+  return r;
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void decode_combine_kernel(const CombineArgs a) {
   using E = Elem<DT>;
-  constexpr int kSplitLanes = 8;
-  __shared__ float s_w[TC_MAX_SPLITS];
-  __shared__ float s_red[kWaves];
-  __shared__ float4 s_o[kSplitLanes][kHeadDim / 4];
+  __shared__ Acc4 s_part[4][kCombineQuads];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int dq = tid & (kCombineQuads - 1);
+  const int sl = tid / kCombineQuads;
   const int G = a.group;
   const int S = a.splits;
-  const int64_t bhg = blockIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int quarter = static_cast<int>(blk & 3);
+  const int64_t bhg = blk >> 2;
   const int g = static_cast<int>(bhg % G);
   const int64_t bh = bhg / G;
   const int h = static_cast<int>(bh % a.heads);
   const int64_t b = bh / a.heads;
+  const int dim0 = 32 * quarter + 4 * dq;
 
   const float* lse = a.lse_part + bh * S * G + g;
-  const float* o = a.o_part + (bh * S * G + g) * kHeadDim;
+  const float* o = a.o_part + (bh * S * G + g) * kHeadDim + dim0;
 
-  float mx = neg_inf();
-  for (int s = tid; s < S; s += 256) mx = fmaxf(mx, lse[static_cast<int64_t>(s) * G]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-  if (lane == 0) s_red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float ms = (mx == neg_inf()) ? 0.f : mx;
-  __syncthreads();
-
-  float sum = 0.f;
-  for (int s = tid; s < S; s += 256) {
-    const float e = __builtin_amdgcn_exp2f((lse[static_cast<int64_t>(s) * G] - ms) * kLog2e);
-    s_w[s] = e;
-    sum += e;
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-  if (lane == 0) s_red[wave] = sum;
-  __syncthreads();
-  sum = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-
-  const int sl = tid >> 5;   // split lane
-  const int dq = tid & 31;   // dims 4*dq .. 4*dq+3
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  Acc4 acc;
+  acc.m = neg_inf();
+  acc.l = 0.f;
+  acc.o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 4
-  for (int s = sl; s < S; s += kSplitLanes) {
-    const float w = s_w[s];
-    const float4 ov = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(s) * G * kHeadDim + 4 * dq);
-    acc.x = fmaf(w, ov.x, acc.x);
-    acc.y = fmaf(w, ov.y, acc.y);
-    acc.z = fmaf(w, ov.z, acc.z);
-    acc.w = fmaf(w, ov.w, acc.w);
+  for (int s = sl; s < S; s += kCombineLanes) {
+    const float ls = lse[static_cast<int64_t>(s) * G];
+    const float4 ov = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(s) * G * kHeadDim);
+    Acc4 one;
+    one.m = ls;
+    one.l = 1.f;
+    one.o = ov;
+    acc = merge(acc, one);
   }
-  s_o[sl][dq] = acc;
+  // Split lanes inside the wave: lanes dq + 8 * k, k = 0..7.
+  acc = merge(acc, shfl_xor(acc, 8));
+  acc = merge(acc, shfl_xor(acc, 16));
+  acc = merge(acc, shfl_xor(acc, 32));
+  if (lane < kCombineQuads) s_part[wave][lane] = acc;
   __syncthreads();
-  if (tid < kHeadDim / 4) {
-    float4 r = s_o[0][tid];
+  if (tid < kCombineQuads) {
+    Acc4 r = s_part[0][tid];
 #pragma unroll
-    for (int k = 1; k < kSplitLanes; ++k) {
-      const float4 t = s_o[k][tid];
-      r.x += t.x; r.y += t.y; r.z += t.z; r.w += t.w;
-    }
-    const bool empty = (mx == neg_inf());
-    const float inv = empty ? 0.f : 1.f / sum;
-    const uint32_t w0 = E::bits(r.x * inv) | (E::bits(r.y * inv) << 16);
-    const uint32_t w1 = E::bits(r.z * inv) | (E::bits(r.w * inv) << 16);
-    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 4 * tid;
+    for (int w = 1; w < 4; ++w) r = merge(r, s_part[w][tid]);
+    const bool empty = (r.m == neg_inf());
+    const float inv = empty ? 0.f : 1.f / r.l;
+    const uint32_t w0 = E::bits(r.o.x * inv) | (E::bits(r.o.y * inv) << 16);
+    const uint32_t w1 = E::bits(r.o.z * inv) | (E::bits(r.o.w * inv) << 16);
+    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 32 * quarter + 4 * tid;
     *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
   }
 }
@@ -519,7 +607,7 @@ int split_tokens_impl(int batch, int kv_heads, int64_t max_tokens, int split_tok
     const int rc = current_device_cus(&cus);
     if (rc != TC_OK) return rc;
     // About two work-groups per compute unit over all (sequence, head) pairs.
-    const int64_t target = 2 * static_cast<int64_t>(cus);
+    const int64_t target = static_cast<int64_t>(TC_DECODE_WGS_PER_CU) * cus;
     t = ceil_div(ceil_div(max_tokens * batch * kv_heads, target), kSplitGranule) * kSplitGranule;
   }
   t = max(t, static_cast<int64_t>(kSplitGranule));
@@ -557,11 +645,15 @@ size_t tc_decode_workspace_bytes(int batch, int kv_heads, int group, int head_di
   return parts * head_dim * sizeof(float) + parts * sizeof(float);
 }
 
-int tc_decode_partial(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
-                      const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
-                      int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
-                      int num_splits, float* o_part_dev, float* lse_part_dev, void* stream) {
-  clear_error();
+}  // extern "C"
+
+namespace tc {
+namespace {
+
+int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                 const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens, int batch,
+                 int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens, int num_splits,
+                 float* o_part_dev, float* lse_part_dev, int interleave, void* stream) {
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens == 0 && num_splits == 0) return TC_OK;  // empty caches: nothing to read
@@ -605,12 +697,27 @@ int tc_decode_partial(const void* q_dev, const int64_t q_strides[3], const void*
   a.group = group;
   a.splits = num_splits;
   a.split_tokens = split_tokens;
+  a.interleave = interleave;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, s)
                                              : launch_partial_dt<TC_DTYPE_BF16>(a, batch, s);
   return hip_status(e, "decode_partial launch");
+}
+
+}  // namespace
+}  // namespace tc
+
+extern "C" {
+
+int tc_decode_partial(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                      const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
+                      int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
+                      int num_splits, float* o_part_dev, float* lse_part_dev, void* stream) {
+  clear_error();
+  return partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
+                      head_dim, dtype, scale, split_tokens, num_splits, o_part_dev, lse_part_dev, 0, stream);
 }
 
 int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int batch, int kv_heads, int group,
@@ -635,7 +742,9 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   a.heads = kv_heads;
   a.group = group;
   a.splits = num_splits;
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(batch) * kv_heads * group));
+  const int64_t blocks = static_cast<int64_t>(batch) * kv_heads * group * 4;
+  if (blocks > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many (sequence, head) pairs");
+  const dim3 grid(static_cast<unsigned>(blocks));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TC_DTYPE_F16)
     hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_F16>), grid, dim3(256), 0, s, a);
@@ -662,8 +771,9 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const voi
   float* o_part = static_cast<float*>(workspace_dev);
   float* lse_part = S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * group * head_dim : nullptr;
   if (S > 0) {
-    rc = tc_decode_partial(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch,
-                           kv_heads, group, head_dim, dtype, scale, t, S, o_part, lse_part, stream);
+    // Splits here are internal, so their tiles are dealt round-robin (the merged result is the same).
+    rc = partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
+                      head_dim, dtype, scale, t, S, o_part, lse_part, TC_DECODE_INTERLEAVE, stream);
     if (rc != TC_OK) return rc;
   }
   return tc_decode_combine(o_part, lse_part, batch, kv_heads, group, head_dim, S, out_dev, out_strides, dtype, stream);

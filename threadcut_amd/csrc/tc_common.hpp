@@ -27,7 +27,7 @@ int hip_status(hipError_t e, const char* what);
 int current_device_cus(int* cus_out);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------
 // Device side: element conversions and wave64 data movement.
