@@ -143,6 +143,102 @@ def bench_splice(dev, steps, warmup):
                                                    "theta": 1e6}}
 
 
+SWEEP = (1536, 4096, 10240, 14336)
+
+
+def summarize(r, nbytes):
+    us = r["ms"] * 1e3 / LAYERS
+    pus = r["ms_partial"] * 1e3 / LAYERS
+    return {"us_per_call": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+            "partial_us": round(pus, 3), "partial_GB/s": round(nbytes / pus / 1e3, 1),
+            "splits": r["splits"], "split_tokens": r["split_tokens"]}
+
+
+def measure_sweep(dev, n, steps, warmup, split, only):
+    """36 sequential decode calls at n tokens (own K/V per layer) as one HIP graph."""
+    import torch
+
+    from threadcut_amd import flash_decode, workloads
+
+    ks, vs = workloads.layer_caches(2, LAYERS, n, device=dev)
+    gq = torch.Generator(device=dev)
+    gq.manual_seed(2)
+    qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+    plans = [flash_decode.DecodePlan(q, k, v, D ** -0.5, o, split=split or None)
+             for q, k, v, o in zip(qs, ks, vs, outs)]
+
+    def step():
+        for p in plans:
+            p.run()
+
+    def step_partial():
+        for p in plans:
+            p.run_partial()
+
+    result = {"splits": plans[0].splits, "split_tokens": plans[0].split_tokens}
+    if only in (None, "decode"):
+        result["ms"] = time_graph(capture(step), steps, warmup)
+    if only in (None, "partial"):
+        result["ms_partial"] = time_graph(capture(step_partial), steps, warmup)
+    del plans, ks, vs
+    torch.cuda.empty_cache()
+    return result
+
+
+def _time_plan(plan, steps, reps=10):
+    def step():
+        for _ in range(reps):
+            plan.run()
+    ms = time_graph(capture(step), steps, 3)
+    return ms * 1e3 / reps
+
+
+def measure_ragged(dev, steps):
+    """16 sequences, lengths U[1024, 32768] (seed 3), one padded cache + int32 lengths."""
+    import torch
+
+    from threadcut_amd import flash_decode, workloads
+
+    gen = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 32769, (16,), generator=gen).to(torch.int32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    k = torch.randn((16, HKV, 32768, D), generator=g, device=dev).half()
+    v = torch.randn((16, HKV, 32768, D), generator=g, device=dev).half()
+    q = torch.randn((16, HKV, HQ // HKV, D), generator=g, device=dev).half()
+    out = torch.empty_like(q)
+    plan = flash_decode.DecodePlan(q, k, v, D ** -0.5, out, lens=lens.to(dev))
+    us = _time_plan(plan, steps)
+    nbytes = int(lens.sum()) * 2 * HKV * D * 2 + 16 * 2 * HQ * D * 2
+    del k, v
+    torch.cuda.empty_cache()
+    return {"us_per_call": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes,
+            "lens_sum": int(lens.sum()), "splits": plan.splits, "split_tokens": plan.split_tokens}
+
+
+def measure_long(dev, batch, steps):
+    """One decode call over 131072 cached tokens per sequence (seed 4)."""
+    import torch
+
+    from threadcut_amd import flash_decode
+
+    n = 131072
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    k = torch.randn((batch, HKV, n, D), generator=g, device=dev).half()
+    v = torch.randn((batch, HKV, n, D), generator=g, device=dev).half()
+    q = torch.randn((batch, HKV, HQ // HKV, D), generator=g, device=dev).half()
+    out = torch.empty_like(q)
+    plan = flash_decode.DecodePlan(q, k, v, D ** -0.5, out)
+    us = _time_plan(plan, steps)
+    nbytes = decode_bytes(n, batch)
+    del k, v
+    torch.cuda.empty_cache()
+    return {"us_per_call": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes,
+            "splits": plan.splits, "split_tokens": plan.split_tokens}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,6 +249,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-splice", action="store_true")
+    ap.add_argument("--no-reports", action="store_true",
+                    help="skip the other lengths, the ragged batch and the 131072-token calls")
     ap.add_argument("--only", choices=["decode", "partial", "splice", "copy"], default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -167,7 +265,7 @@ def main():
 
     import torch
 
-    from threadcut_amd import flash_decode, workloads
+    import threadcut_amd  # noqa: F401  (fails loudly here if the package is broken)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -185,34 +283,9 @@ def main():
         return
 
     n = args.n
-    scale = D ** -0.5
-    ks, vs = workloads.layer_caches(2, LAYERS, n, device=dev)
-    gq = torch.Generator(device=dev)
-    gq.manual_seed(2)
-    qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
-    outs = [torch.empty_like(q) for q in qs]
-    plans = [flash_decode.DecodePlan(q, k, v, scale, o, split=args.split or None)
-             for q, k, v, o in zip(qs, ks, vs, outs)]
-
-    def step():
-        for p in plans:
-            p.run()
-
-    def step_partial():
-        for p in plans:
-            p.run_partial()
-
-    result = {}
-    if args.only in (None, "decode"):
-        g = capture(step)
-        ms = time_graph(g, args.steps, args.warmup)
-        result["ms"] = ms
-    if args.only in (None, "partial"):
-        gp = capture(step_partial)
-        ms_p = time_graph(gp, args.steps, args.warmup)
-        result["ms_partial"] = ms_p
+    result = measure_sweep(dev, n, args.steps, args.warmup, args.split, args.only)
     if args.only is not None:
-        print(json.dumps({k: round(v, 5) for k, v in result.items()}))
+        print(json.dumps({k: round(v, 5) for k, v in result.items() if isinstance(v, float)}))
         return
 
     ms = result["ms"]
@@ -238,13 +311,21 @@ def main():
         "config": {"workload": f"36-layer decode sweep at {n} tokens, Qwen3-4B GQA (32 q / 8 kv heads, D=128), "
                                f"batch 1, one HIP graph per step",
                    "layers": LAYERS, "kv_tokens": n, "batch": 1, "q_heads": HQ, "kv_heads": HKV,
-                   "head_dim": D, "splits": plans[0].splits, "split_tokens": plans[0].split_tokens},
+                   "head_dim": D, "splits": result["splits"], "split_tokens": result["split_tokens"]},
         "roofline": {"bound": "hbm", "kernel": "decode_partial_kernel<f16, g=4>",
                      "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "us_per_launch": round(partial_us, 3),
                      "bytes_per_launch": per_call_bytes,
                      "traffic": read_traffic(f"decode_partial_n{n}_traffic.txt")},
     }
+    if not args.no_reports:
+        sweep = {}
+        for m in SWEEP:
+            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None)
+            sweep[str(m)] = summarize(r, decode_bytes(m))
+        line["sweep_36_layers"] = sweep
+        line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
+        line["long_131072"] = {f"B{b}": measure_long(dev, b, max(10, args.steps // 10)) for b in (1, 4)}
     if not args.no_splice:
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:
