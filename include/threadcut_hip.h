@@ -73,14 +73,17 @@ int tc_abi_version(void);
 /* dtype, fp32 accumulation throughout.                                      */
 /* ------------------------------------------------------------------------ */
 
-/* Number of KV splits a call with these sizes uses. split_tokens <= 0 lets
- * the library choose the split length so that B*Hkv*S work-groups fill the
- * device; a positive value is rounded up to the kernel's token granule (64).
- * Host-only; needs no GPU when split_tokens > 0. */
-int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_tokens);
+/* Number of KV splits S a call with these sizes uses (a negative value is
+ * -TC_ERR_*). split_tokens <= 0 lets the library choose S so that the
+ * B*Hkv*S work-groups match the device's compute units (more of them when
+ * `ragged`, i.e. when per-sequence lengths are passed); a positive value is a
+ * split length in tokens, rounded up to the kernel's granule (64), as the
+ * reference's `split` (threadcut/flash_decode.py:57,61). Host-only; needs no
+ * GPU when split_tokens > 0. */
+int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int ragged);
 
-/* Tokens per split that a call with these sizes uses (see above). */
-int tc_decode_split_tokens(int batch, int kv_heads, int64_t max_tokens, int split_tokens);
+/* Tokens per split of the same plan (S * tokens >= max_tokens). */
+int tc_decode_split_tokens(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int ragged);
 
 /* Bytes of device workspace for num_splits splits: fp32 partial outputs
  * [B, Hkv, S, G, D] followed by fp32 partial log-sum-exps [B, Hkv, S, G]. */
@@ -105,9 +108,11 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev,
                       void* out_dev, const int64_t out_strides[3], int dtype, void* stream);
 
 /* Both passes. workspace_dev must hold tc_decode_workspace_bytes(...) bytes
- * for the split count tc_decode_num_splits(batch, kv_heads, max_tokens,
- * split_tokens) where max_tokens = n_tokens. With lens_dev != NULL every
- * lens[b] must be in [0, n_tokens]. */
+ * for the split count tc_decode_num_splits(batch, kv_heads, n_tokens,
+ * split_tokens, lens_dev != NULL). Lengths past n_tokens are clamped to it.
+ * Here the splits are internal, so each takes every S-th 16-token tile of a
+ * head (the loads in flight stay adjacent in HBM); the merged output is the
+ * same as with contiguous slices. */
 int tc_decode_attention(const void* q_dev, const int64_t q_strides[3],
                         const void* k_dev, const int64_t k_strides[3],
                         const void* v_dev, const int64_t v_strides[3],

@@ -40,16 +40,16 @@ def test_version_and_messages(lib):
 
 
 def test_split_arithmetic(lib):
-    assert lib.tc_decode_split_tokens(1, 8, 10240, 256) == 256
-    assert lib.tc_decode_num_splits(1, 8, 10240, 256) == 40      # cdiv(n, split) as the reference
-    assert lib.tc_decode_split_tokens(1, 8, 10240, 100) == 128   # rounded up to the 64-token granule
-    assert lib.tc_decode_num_splits(1, 8, 10240, 100) == 80
-    assert lib.tc_decode_num_splits(1, 8, 0, 256) == 0
+    assert lib.tc_decode_split_tokens(1, 8, 10240, 256, 0) == 256
+    assert lib.tc_decode_num_splits(1, 8, 10240, 256, 0) == 40      # cdiv(n, split) as the reference
+    assert lib.tc_decode_split_tokens(1, 8, 10240, 100, 0) == 128   # rounded up to the 64-token granule
+    assert lib.tc_decode_num_splits(1, 8, 10240, 100, 1) == 80
+    assert lib.tc_decode_num_splits(1, 8, 0, 256, 0) == 0
     # Never more than TC_MAX_SPLITS splits: the split grows instead.
     n = 1 << 24
-    assert lib.tc_decode_num_splits(1, 8, n, 64) <= _lib.TC_MAX_SPLITS
-    assert lib.tc_decode_split_tokens(1, 8, n, 64) == n // _lib.TC_MAX_SPLITS
-    assert lib.tc_decode_num_splits(0, 8, 100, 64) == -_lib.TC_ERR_INVALID_ARGUMENT
+    assert lib.tc_decode_num_splits(1, 8, n, 64, 0) <= _lib.TC_MAX_SPLITS
+    assert lib.tc_decode_split_tokens(1, 8, n, 64, 0) == n // _lib.TC_MAX_SPLITS
+    assert lib.tc_decode_num_splits(0, 8, 100, 64, 0) == -_lib.TC_ERR_INVALID_ARGUMENT
 
 
 def test_workspace_bytes(lib):

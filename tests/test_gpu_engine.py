@@ -1,0 +1,96 @@
+"""Drop-in through transformers on the GPU: a small random Qwen3 (head_dim 128,
+8 query heads over 2 KV heads, fp16) run with the registered "threadcut"
+attention and the GrowingLayer cache, against stock SDPA.
+
+Mirrors the reference's engine tests (threadcut's tests/test_core.py): T3's
+decode-equals-stock-transformers check, compared here on teacher-forced logits
+(a random model's near-ties make greedy tokens a fragile oracle), and T2's
+splice-equals-fresh-compute check with the reference's 3e-2 fp16 tolerance.
+"""
+import pytest
+import torch
+from transformers import AutoModelForCausalLM, DynamicCache, Qwen3Config
+
+from threadcut_amd import attention, kv
+from threadcut_amd.match import Split, split
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 3e-2
+
+
+@pytest.fixture(scope="module")
+def model(gpu):
+    torch.manual_seed(0)
+    cfg = Qwen3Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=4096,
+                      rope_theta=1e6)
+    m = AutoModelForCausalLM.from_config(cfg, dtype=torch.float16, attn_implementation=attention.NAME)
+    return m.to(gpu).eval()
+
+
+def rand_ids(n, seed, vocab=500):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(10, vocab, (n,), generator=g).tolist()
+
+
+def run(m, ids, cache, impl, start=None):
+    m.set_attn_implementation(impl)
+    x = torch.tensor([ids], device=m.device)
+    kw = {}
+    if start is not None:
+        kw["position_ids"] = torch.arange(start, start + len(ids), device=m.device)[None]
+    return m(input_ids=x, past_key_values=cache, use_cache=True, **kw).logits[0, -1].float()
+
+
+def kv_alone(m, ids, start):
+    """KV of `ids` at positions start.. with no other context visible (stock SDPA)."""
+    cache = DynamicCache(config=m.config)
+    run(m, ids, cache, "sdpa", start)
+    return cache
+
+
+@torch.no_grad()
+def test_decode_steps_match_stock_sdpa(model):
+    """Prefill 40 tokens, then 12 single-token steps: every step's logits vs stock SDPA."""
+    ids = rand_ids(52, 5)
+    ours = kv.new_cache(model.config)
+    ref = DynamicCache(config=model.config)
+    run(model, ids[:40], ours, attention.NAME)
+    run(model, ids[:40], ref, "sdpa")
+    for t in ids[40:]:
+        a = run(model, [t], ours, attention.NAME)
+        b = run(model, [t], ref, "sdpa")
+        assert (a - b).abs().max().item() <= ATOL
+    assert ours.get_seq_length() == 52
+
+
+@torch.no_grad()
+def test_splice_matches_fresh_compute(model):
+    """T2: cache A·B·C (each span computed alone) spliced to A·C, then D and one decode step."""
+    A, B, C, D = rand_ids(9, 1), rand_ids(13, 2), rand_ids(11, 3), rand_ids(5, 4)
+    inv = model.model.rotary_emb.inv_freq
+    fresh = kv_alone(model, A, 0)
+    c_alone = kv_alone(model, C, len(A))
+    for lo, li in zip(fresh.layers, c_alone.layers):
+        lo.keys = torch.cat((lo.keys, li.keys), 2)
+        lo.values = torch.cat((lo.values, li.values), 2)
+    ref_logits = run(model, D, fresh, "sdpa")
+
+    cache = kv.new_cache(model.config)
+    for span, start in ((A, 0), (B, len(A)), (C, len(A) + len(B))):
+        part = kv_alone(model, span, start)
+        for layer, p in zip(cache.layers, part.layers):
+            layer.update(p.keys, p.values)
+    s = split(A + B + C, A + C + D, min_suffix=4)
+    assert s == Split(len(A), len(A) + len(B), len(C))
+    kv.splice(cache, s, inv)
+    assert cache.get_seq_length() == len(A) + len(C)
+    logits = run(model, D, cache, attention.NAME)
+    assert (logits - ref_logits).abs().max().item() <= ATOL
+
+    # One decode step on the spliced cache goes through the HIP decode kernel.
+    nxt = int(ref_logits.argmax())
+    got = run(model, [nxt], cache, attention.NAME)
+    want = run(model, [nxt], fresh, "sdpa")
+    assert (got - want).abs().max().item() <= ATOL

@@ -39,8 +39,8 @@ SIGNATURES = {
     "tc_strerror": (ctypes.c_char_p, [_I]),
     "tc_last_error": (ctypes.c_char_p, []),
     "tc_abi_version": (_I, []),
-    "tc_decode_num_splits": (_I, [_I, _I, _I64, _I]),
-    "tc_decode_split_tokens": (_I, [_I, _I, _I64, _I]),
+    "tc_decode_num_splits": (_I, [_I, _I, _I64, _I, _I]),
+    "tc_decode_split_tokens": (_I, [_I, _I, _I64, _I, _I]),
     "tc_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "tc_decode_partial": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I,
                                _P, _P, _P]),

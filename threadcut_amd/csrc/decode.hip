@@ -23,6 +23,8 @@
 // work-group writes one (o, lse) partial per query head.
 #include <math.h>
 
+#include <algorithm>
+
 #include "tc_common.hpp"
 
 namespace tc {
@@ -44,6 +46,12 @@ namespace {
 #ifndef TC_DECODE_INTERLEAVE
 #define TC_DECODE_INTERLEAVE 1  // tc_decode_attention deals tiles round-robin over the splits
 #endif
+#ifndef TC_DECODE_WAVE_PARTIALS
+#define TC_DECODE_WAVE_PARTIALS 0  // 1: every wave writes its own partial (no LDS merge)
+#endif
+#ifndef TC_DECODE_RAGGED_WGS_PER_CU
+#define TC_DECODE_RAGGED_WGS_PER_CU 8  // the same with per-sequence lengths: finer splits balance them
+#endif
 #ifndef TC_DECODE_WGS_PER_CU
 #define TC_DECODE_WGS_PER_CU 1  // partial work-groups per compute unit the split heuristic aims at
 #endif
@@ -52,6 +60,7 @@ constexpr int kHeadDim = 128;
 constexpr int kWaves = TC_DECODE_WAVES;
 constexpr int kDepth = TC_DECODE_DEPTH;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
+constexpr int kPartsPerSplit = TC_DECODE_WAVE_PARTIALS ? kWaves : 1;  // (o, lse) partials per split
 constexpr int kSplitGranule = kWaves * kWaveIter > 64 ? kWaves * kWaveIter : 64;  // split length granule
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -429,6 +438,27 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     mh[hh] = M;
   }
 
+#if TC_DECODE_WAVE_PARTIALS
+  // Every wave writes its own partial (part index split * kWaves + wave).
+  {
+    const int64_t part = ((static_cast<int64_t>(b) * a.heads + h) * a.splits + split) * kWaves + wave;
+    if (grp == 0) {
+#pragma unroll
+      for (int hh = 0; hh < GP; ++hh) {
+        if (hh < a.group) {
+          const float inv = 1.f / (lh[hh] == 0.f ? 1.f : lh[hh]);
+          float4* dst = reinterpret_cast<float4*>(a.o_part + (part * a.group + hh) * kHeadDim + 8 * c);
+          dst[0] = make_float4(st.acc[hh][0] * inv, st.acc[hh][1] * inv, st.acc[hh][2] * inv, st.acc[hh][3] * inv);
+          dst[1] = make_float4(st.acc[hh][4] * inv, st.acc[hh][5] * inv, st.acc[hh][6] * inv, st.acc[hh][7] * inv);
+          if (c == 0)
+            a.lse_part[part * a.group + hh] =
+                (lh[hh] == 0.f) ? neg_inf() : (mh[hh] + __log2f(lh[hh])) * kLn2;
+        }
+      }
+    }
+    return;
+  }
+#endif
   // Merge the waves through LDS and write this split's partial.
   if (grp == 0) {
 #pragma unroll
@@ -593,27 +623,41 @@ hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream
   return launch_partial_t<DT, 8>(a, batch, stream);
 }
 
-int split_tokens_impl(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int* out) {
+// Split plan of a call: S splits of T tokens each (S * T >= n, T a multiple of
+// the granule). With split_tokens > 0 the caller fixes T. Otherwise S is
+// chosen so that B * Hkv * S work-groups are TC_DECODE_WGS_PER_CU per compute
+// unit (every work-group then streams the same share of the cache when its
+// tiles are dealt round-robin), but never more splits than a head has
+// wave-tiles and never more than TC_MAX_SPLITS. Ragged batches (per-sequence
+// lengths) aim at TC_DECODE_RAGGED_WGS_PER_CU per unit: short sequences leave
+// their work-groups light, and many small work-groups let the dispatcher
+// balance the rest.
+int split_plan(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int ragged, int* S_out, int* T_out) {
   if (batch < 1 || kv_heads < 1 || max_tokens < 0)
     return fail(TC_ERR_INVALID_ARGUMENT, "split query with batch %d, kv_heads %d, max_tokens %lld", batch, kv_heads,
                 (long long)max_tokens);
   // Shortest split that keeps the split count within TC_MAX_SPLITS.
   const int64_t floor_t = ceil_div(ceil_div(max_tokens, TC_MAX_SPLITS), kSplitGranule) * kSplitGranule;
-  int64_t t;
+  int64_t t, S;
   if (split_tokens > 0) {
-    t = ceil_div(split_tokens, kSplitGranule) * kSplitGranule;
+    t = max(ceil_div(split_tokens, kSplitGranule) * kSplitGranule, floor_t);
+    S = ceil_div(max_tokens, t);
   } else {
     int cus = 0;
     const int rc = current_device_cus(&cus);
     if (rc != TC_OK) return rc;
-    // About two work-groups per compute unit over all (sequence, head) pairs.
-    const int64_t target = static_cast<int64_t>(TC_DECODE_WGS_PER_CU) * cus;
-    t = ceil_div(ceil_div(max_tokens * batch * kv_heads, target), kSplitGranule) * kSplitGranule;
+    const int64_t target = static_cast<int64_t>(ragged ? TC_DECODE_RAGGED_WGS_PER_CU : TC_DECODE_WGS_PER_CU) * cus;
+    const int64_t per_head = static_cast<int64_t>(batch) * kv_heads;
+    const int64_t max_s = std::max<int64_t>(1, std::min<int64_t>(ceil_div(ceil_div(max_tokens, kWaveIter), kWaves),
+                                                        TC_MAX_SPLITS));
+    S = std::max<int64_t>(1, std::min<int64_t>((target + per_head / 2) / per_head, max_s));
+    t = max(ceil_div(ceil_div(max_tokens, S), kSplitGranule) * kSplitGranule, floor_t);
+    if (max_tokens == 0) S = 0;
   }
   t = max(t, static_cast<int64_t>(kSplitGranule));
-  t = max(t, floor_t);
   if (t > (1 << 30)) return fail(TC_ERR_INVALID_ARGUMENT, "split length %lld too large", (long long)t);
-  *out = static_cast<int>(t);
+  *S_out = static_cast<int>(S);
+  *T_out = static_cast<int>(t);
   return TC_OK;
 }
 
@@ -624,24 +668,23 @@ using namespace tc;
 
 extern "C" {
 
-int tc_decode_split_tokens(int batch, int kv_heads, int64_t max_tokens, int split_tokens) {
+int tc_decode_split_tokens(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int ragged) {
   clear_error();
-  int t = 0;
-  const int rc = split_tokens_impl(batch, kv_heads, max_tokens, split_tokens, &t);
+  int S = 0, t = 0;
+  const int rc = split_plan(batch, kv_heads, max_tokens, split_tokens, ragged, &S, &t);
   return rc == TC_OK ? t : -rc;
 }
 
-int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_tokens) {
+int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int ragged) {
   clear_error();
-  int t = 0;
-  const int rc = split_tokens_impl(batch, kv_heads, max_tokens, split_tokens, &t);
-  if (rc != TC_OK) return -rc;
-  return static_cast<int>(ceil_div(max_tokens, t));
+  int S = 0, t = 0;
+  const int rc = split_plan(batch, kv_heads, max_tokens, split_tokens, ragged, &S, &t);
+  return rc == TC_OK ? S : -rc;
 }
 
 size_t tc_decode_workspace_bytes(int batch, int kv_heads, int group, int head_dim, int num_splits) {
   if (batch < 1 || kv_heads < 1 || group < 1 || head_dim < 1 || num_splits < 0) return 0;
-  const size_t parts = static_cast<size_t>(batch) * kv_heads * num_splits * group;
+  const size_t parts = static_cast<size_t>(batch) * kv_heads * num_splits * kPartsPerSplit * group;
   return parts * head_dim * sizeof(float) + parts * sizeof(float);
 }
 
@@ -741,7 +784,7 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   a.so_b = out_strides[0]; a.so_h = out_strides[1]; a.so_g = out_strides[2];
   a.heads = kv_heads;
   a.group = group;
-  a.splits = num_splits;
+  a.splits = num_splits * kPartsPerSplit;
   const int64_t blocks = static_cast<int64_t>(batch) * kv_heads * group * 4;
   if (blocks > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many (sequence, head) pairs");
   const dim3 grid(static_cast<unsigned>(blocks));
@@ -762,14 +805,14 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const voi
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
-  int t = 0;
-  if ((rc = split_tokens_impl(batch, kv_heads, n_tokens, split_tokens, &t)) != TC_OK) return rc;
-  const int S = static_cast<int>(ceil_div(n_tokens, t));
+  int S = 0, t = 0;
+  if ((rc = split_plan(batch, kv_heads, n_tokens, split_tokens, lens_dev != nullptr, &S, &t)) != TC_OK) return rc;
   const size_t need = tc_decode_workspace_bytes(batch, kv_heads, group, head_dim, S);
   if (S > 0 && (!workspace_dev || workspace_bytes < need))
     return fail(TC_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, need, S);
   float* o_part = static_cast<float*>(workspace_dev);
-  float* lse_part = S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * group * head_dim : nullptr;
+  float* lse_part =
+      S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * kPartsPerSplit * group * head_dim : nullptr;
   if (S > 0) {
     // Splits here are internal, so their tiles are dealt round-robin (the merged result is the same).
     rc = partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,

@@ -21,7 +21,13 @@ constexpr int kHeadDim = 128;
 constexpr int kHalf = kHeadDim / 2;
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = kThreads / 8;
-constexpr int kUnroll = 4;
+#ifndef TC_SPLICE_UNROLL
+#define TC_SPLICE_UNROLL 4  // passes of loads a thread keeps in flight
+#endif
+#ifndef TC_SPLICE_NT
+#define TC_SPLICE_NT 1      // non-temporal loads and stores (the strips are touched once)
+#endif
+constexpr int kUnroll = TC_SPLICE_UNROLL;
 constexpr int kTileRows = kRowsPerPass * kUnroll;  // rows per work-group tile
 constexpr int kMaxJobs = 128;                      // strips sets per launch (64 layers x K,V)
 
@@ -36,6 +42,26 @@ struct SpliceArgs {
   int rot_jobs;    // jobs [0, rot_jobs) are keys (rotated), the rest copied
   int sequential;  // 1: one work-group walks a whole strip in row order
 };
+
+__device__ __forceinline__ uint4 load16(const uint16_t* p) {
+#if TC_SPLICE_NT
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
+__device__ __forceinline__ void store16(uint16_t* p, const uint4& x) {
+#if TC_SPLICE_NT
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  v4u v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(p));
+#else
+  *reinterpret_cast<uint4*>(p) = x;
+#endif
+}
 
 // out = fp(fl(x*cos) + fl(rotate_half(x)*sin)) per element, no contraction:
 // lower half  y = x_lo*cos - x_hi*sin,  upper half y = x_hi*cos + x_lo*sin.
@@ -92,8 +118,8 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
       const int64_t r = row + i * kRowsPerPass + r_in;
       if (r < row_end) {
         const uint16_t* p = src + (a.src_row0 + r) * a.ss_t;
-        lo[i] = *reinterpret_cast<const uint4*>(p);
-        hi[i] = *reinterpret_cast<const uint4*>(p + kHalf);
+        lo[i] = load16(p);
+        hi[i] = load16(p + kHalf);
       }
     }
     if (a.sequential) {
@@ -108,8 +134,8 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
       if (r < row_end) {
         if (rot) rotate_pair<DT>(lo[i], hi[i], cv, sv);
         uint16_t* p = dst + (a.dst_row0 + r) * a.ds_t;
-        *reinterpret_cast<uint4*>(p) = lo[i];
-        *reinterpret_cast<uint4*>(p + kHalf) = hi[i];
+        store16(p, lo[i]);
+        store16(p + kHalf, hi[i]);
       }
     }
   }

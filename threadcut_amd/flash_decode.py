@@ -18,19 +18,19 @@ HEAD_DIM = 128
 SPLIT_GRANULE = 64  # tokens; split lengths are rounded up to this
 
 
-def num_splits(batch, kv_heads, n_tokens, split=None):
+def num_splits(batch, kv_heads, n_tokens, split=None, ragged=False):
     """KV splits a call of this size uses (``split=None``: tuned to fill the GPU)."""
     lib = _lib.load()
-    s = lib.tc_decode_num_splits(int(batch), int(kv_heads), int(n_tokens), int(split or 0))
+    s = lib.tc_decode_num_splits(int(batch), int(kv_heads), int(n_tokens), int(split or 0), int(bool(ragged)))
     if s < 0:
         _lib.check(-s, "tc_decode_num_splits")
     return s
 
 
-def split_tokens(batch, kv_heads, n_tokens, split=None):
+def split_tokens(batch, kv_heads, n_tokens, split=None, ragged=False):
     """Tokens per split a call of this size uses."""
     lib = _lib.load()
-    t = lib.tc_decode_split_tokens(int(batch), int(kv_heads), int(n_tokens), int(split or 0))
+    t = lib.tc_decode_split_tokens(int(batch), int(kv_heads), int(n_tokens), int(split or 0), int(bool(ragged)))
     if t < 0:
         _lib.check(-t, "tc_decode_split_tokens")
     return t
@@ -81,7 +81,7 @@ def decode_into(q, k, v, scale, out, lens=None, split=None):
     lib = _lib.load()
     dt = _lib.dtype_code(q.dtype)
     with torch.cuda.device(q.device):
-        s = num_splits(b, hkv, n, split)
+        s = num_splits(b, hkv, n, split, ragged=lens is not None)
         nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
         rc = lib.tc_decode_attention(
@@ -125,8 +125,9 @@ class DecodePlan:
         self.lib = _lib.load()
         self.device = q.device
         with torch.cuda.device(q.device):
-            self.splits = num_splits(b, hkv, k.shape[2], split)
-            self.split_tokens = split_tokens(b, hkv, k.shape[2], split)
+            ragged = lens is not None
+            self.splits = num_splits(b, hkv, k.shape[2], split, ragged)
+            self.split_tokens = split_tokens(b, hkv, k.shape[2], split, ragged)
             nbytes = self.lib.tc_decode_workspace_bytes(b, hkv, g, d, self.splits)
             self.workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
         self.tensors = (q, k, v, out, lens)
