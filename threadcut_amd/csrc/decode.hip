@@ -46,9 +46,6 @@ namespace {
 #ifndef TC_DECODE_INTERLEAVE
 #define TC_DECODE_INTERLEAVE 1  // tc_decode_attention deals tiles round-robin over the splits
 #endif
-#ifndef TC_DECODE_WAVE_PARTIALS
-#define TC_DECODE_WAVE_PARTIALS 0  // 1: every wave writes its own partial (no LDS merge)
-#endif
 #ifndef TC_DECODE_RAGGED_WGS_PER_CU
 #define TC_DECODE_RAGGED_WGS_PER_CU 8  // the same with per-sequence lengths: finer splits balance them
 #endif
@@ -60,7 +57,6 @@ constexpr int kHeadDim = 128;
 constexpr int kWaves = TC_DECODE_WAVES;
 constexpr int kDepth = TC_DECODE_DEPTH;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
-constexpr int kPartsPerSplit = TC_DECODE_WAVE_PARTIALS ? kWaves : 1;  // (o, lse) partials per split
 constexpr int kSplitGranule = kWaves * kWaveIter > 64 ? kWaves * kWaveIter : 64;  // split length granule
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -438,27 +434,6 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     mh[hh] = M;
   }
 
-#if TC_DECODE_WAVE_PARTIALS
-  // Every wave writes its own partial (part index split * kWaves + wave).
-  {
-    const int64_t part = ((static_cast<int64_t>(b) * a.heads + h) * a.splits + split) * kWaves + wave;
-    if (grp == 0) {
-#pragma unroll
-      for (int hh = 0; hh < GP; ++hh) {
-        if (hh < a.group) {
-          const float inv = 1.f / (lh[hh] == 0.f ? 1.f : lh[hh]);
-          float4* dst = reinterpret_cast<float4*>(a.o_part + (part * a.group + hh) * kHeadDim + 8 * c);
-          dst[0] = make_float4(st.acc[hh][0] * inv, st.acc[hh][1] * inv, st.acc[hh][2] * inv, st.acc[hh][3] * inv);
-          dst[1] = make_float4(st.acc[hh][4] * inv, st.acc[hh][5] * inv, st.acc[hh][6] * inv, st.acc[hh][7] * inv);
-          if (c == 0)
-            a.lse_part[part * a.group + hh] =
-                (lh[hh] == 0.f) ? neg_inf() : (mh[hh] + __log2f(lh[hh])) * kLn2;
-        }
-      }
-    }
-    return;
-  }
-#endif
   // Merge the waves through LDS and write this split's partial.
   if (grp == 0) {
 #pragma unroll
@@ -684,7 +659,7 @@ int tc_decode_num_splits(int batch, int kv_heads, int64_t max_tokens, int split_
 
 size_t tc_decode_workspace_bytes(int batch, int kv_heads, int group, int head_dim, int num_splits) {
   if (batch < 1 || kv_heads < 1 || group < 1 || head_dim < 1 || num_splits < 0) return 0;
-  const size_t parts = static_cast<size_t>(batch) * kv_heads * num_splits * kPartsPerSplit * group;
+  const size_t parts = static_cast<size_t>(batch) * kv_heads * num_splits * group;
   return parts * head_dim * sizeof(float) + parts * sizeof(float);
 }
 
@@ -784,7 +759,7 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   a.so_b = out_strides[0]; a.so_h = out_strides[1]; a.so_g = out_strides[2];
   a.heads = kv_heads;
   a.group = group;
-  a.splits = num_splits * kPartsPerSplit;
+  a.splits = num_splits;
   const int64_t blocks = static_cast<int64_t>(batch) * kv_heads * group * 4;
   if (blocks > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many (sequence, head) pairs");
   const dim3 grid(static_cast<unsigned>(blocks));
@@ -812,7 +787,7 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const voi
     return fail(TC_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, need, S);
   float* o_part = static_cast<float*>(workspace_dev);
   float* lse_part =
-      S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * kPartsPerSplit * group * head_dim : nullptr;
+      S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * group * head_dim : nullptr;
   if (S > 0) {
     // Splits here are internal, so their tiles are dealt round-robin (the merged result is the same).
     rc = partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
