@@ -239,6 +239,53 @@ def measure_long(dev, batch, steps):
             "splits": plan.splits, "split_tokens": plan.split_tokens}
 
 
+def measure_append(dev, n, steps):
+    """One decode token over 36 layers at n tokens, cache append included: the
+    reference's order (two strided copies into the cache, then attention) vs
+    the fused append-and-attend launch."""
+    import torch
+
+    from threadcut_amd import _lib, flash_decode
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    cap = n + 64
+    ks = [torch.randn((1, HKV, cap, D), generator=g, device=dev).half() for _ in range(LAYERS)]
+    vs = [torch.randn((1, HKV, cap, D), generator=g, device=dev).half() for _ in range(LAYERS)]
+    kn = [torch.randn((1, HKV, 1, D), generator=g, device=dev).half() for _ in range(LAYERS)]
+    vn = [torch.randn((1, HKV, 1, D), generator=g, device=dev).half() for _ in range(LAYERS)]
+    qs = [torch.randn((1, HKV, HQ // HKV, D), generator=g, device=dev).half() for _ in range(LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+    plans = [flash_decode.DecodePlan(q, k[:, :, :n], v[:, :, :n], D ** -0.5, o)
+             for q, k, v, o in zip(qs, ks, vs, outs)]
+    lib = _lib.load()
+    ws = plans[0].workspace
+    st = _lib.i64x3(*ks[0].stride()[:3])
+    nst = _lib.i64x2(0, kn[0].stride(1))
+    qst = _lib.i64x3(0, qs[0].stride(1), qs[0].stride(2))
+
+    def plain():
+        for k, v, a, b_, p in zip(ks, vs, kn, vn, plans):
+            k[:, :, n - 1:n] = a
+            v[:, :, n - 1:n] = b_
+            p.run()
+
+    def fused():
+        s = _lib.stream_of(dev)
+        for k, v, a, b_, q, o in zip(ks, vs, kn, vn, qs, outs):
+            _lib.check(lib.tc_decode_append_attention(
+                q.data_ptr(), qst, k.data_ptr(), st, v.data_ptr(), st, a.data_ptr(), nst, b_.data_ptr(), nst,
+                n, 1, HKV, HQ // HKV, D, _lib.TC_DTYPE_F16, D ** -0.5, plans[0].split_tokens,
+                ws.data_ptr(), ws.numel(), o.data_ptr(), qst, s), "tc_decode_append_attention")
+
+    ms_plain = time_graph(capture(plain), steps, 5)
+    ms_fused = time_graph(capture(fused), steps, 5)
+    del ks, vs
+    torch.cuda.empty_cache()
+    return {"kv_tokens": n, "us_per_layer_copy_then_attend": round(ms_plain * 1e3 / LAYERS, 3),
+            "us_per_layer_fused_append": round(ms_fused * 1e3 / LAYERS, 3)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -326,6 +373,7 @@ def main():
         line["sweep_36_layers"] = sweep
         line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
         line["long_131072"] = {f"B{b}": measure_long(dev, b, max(10, args.steps // 10)) for b in (1, 4)}
+        line["decode_append"] = measure_append(dev, n, max(20, args.steps // 4))
     if not args.no_splice:
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:

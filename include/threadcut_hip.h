@@ -122,6 +122,25 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3],
                         void* workspace_dev, size_t workspace_bytes,
                         void* out_dev, const int64_t out_strides[3], void* stream);
 
+/* Append-and-attend for one decode step. The new token's K/V rows k_new /
+ * v_new [B, Hkv, D] (element strides (batch, head), last dim contiguous) are
+ * written to row n_tokens - 1 of k_cache / v_cache, and the query attends over
+ * all n_tokens as tc_decode_attention does: the first n_tokens - 1 from the
+ * cache, the last straight from k_new / v_new (so no row is read while it is
+ * written). Workspace as tc_decode_attention(..., ragged = 0). This replaces
+ * GrowingLayer.update's two strided copies per layer per token
+ * (threadcut/kv.py:68-77) together with the decode attention call; the
+ * reference has no fused counterpart. */
+int tc_decode_append_attention(const void* q_dev, const int64_t q_strides[3],
+                               void* k_cache_dev, const int64_t k_strides[3],
+                               void* v_cache_dev, const int64_t v_strides[3],
+                               const void* k_new_dev, const int64_t k_new_strides[2],
+                               const void* v_new_dev, const int64_t v_new_strides[2],
+                               int64_t n_tokens, int batch, int kv_heads, int group, int head_dim,
+                               int dtype, float scale, int split_tokens,
+                               void* workspace_dev, size_t workspace_bytes,
+                               void* out_dev, const int64_t out_strides[3], void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* RoPE delta-shift and suffix splice                                        */
 /*                                                                           */

@@ -195,3 +195,24 @@ def test_rejects_bad_inputs(gpu):
     q, k, v, _ = workloads.decode_inputs(16, n=64)
     with pytest.raises(RuntimeError, match="GPU"):
         flash_decode.decode_attention(q.reshape(8, 4, 128), k[0], v[0], SCALE)
+
+
+@pytest.mark.parametrize("n", [1, 2, 17, 1501, 10240])
+def test_append_attention_writes_the_row_and_attends_over_it(gpu, n):
+    """tc_decode_append_attention: new K/V row written at n - 1, output as if it were in the cache."""
+    cap = n + 37
+    q, k, v, _ = workloads.decode_inputs(30 + n, n=cap)
+    g_ = torch.Generator().manual_seed(31)
+    k_new = torch.randn(1, 8, 1, 128, generator=g_).half()
+    v_new = torch.randn(1, 8, 1, 128, generator=g_).half()
+    kc, vc = k.to(gpu), v.to(gpu)
+    out = torch.empty((1, 8, 4, 128), dtype=torch.float16, device=gpu)
+    flash_decode.decode_append_into(q.to(gpu).reshape(1, 8, 4, 128), kc, vc, k_new.to(gpu), v_new.to(gpu), n,
+                                    SCALE, out)
+    torch.cuda.synchronize()
+    k_ref, v_ref = k.clone(), v.clone()
+    k_ref[:, :, n - 1] = k_new[:, :, 0]
+    v_ref[:, :, n - 1] = v_new[:, :, 0]
+    assert torch.equal(kc.cpu(), k_ref) and torch.equal(vc.cpu(), v_ref)   # only row n - 1 changed
+    ref = f64_ref(q, k_ref[:, :, :n], v_ref[:, :, :n])
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL

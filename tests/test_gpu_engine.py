@@ -94,3 +94,31 @@ def test_splice_matches_fresh_compute(model):
     got = run(model, [nxt], cache, attention.NAME)
     want = run(model, [nxt], fresh, "sdpa")
     assert (got - want).abs().max().item() <= ATOL
+
+
+@torch.no_grad()
+def test_fused_append_cache_matches_plain_cache(model):
+    """new_cache(fused_append=True): the attention kernel writes each decode token's K/V
+    while it attends; logits and cache contents equal the copying cache's."""
+    ids = rand_ids(30, 7)
+    fused = kv.new_cache(model.config, fused_append=True)
+    plain = kv.new_cache(model.config)
+    ref = DynamicCache(config=model.config)
+    for cache, impl in ((fused, attention.NAME), (plain, attention.NAME), (ref, "sdpa")):
+        run(model, ids[:20], cache, impl)
+    for t in ids[20:]:
+        a = run(model, [t], fused, attention.NAME)
+        b = run(model, [t], plain, attention.NAME)
+        c = run(model, [t], ref, "sdpa")
+        # The new token is attended in its own tile, so the fp32 summation order differs slightly.
+        assert (a - b).abs().max().item() <= ATOL
+        assert (a - c).abs().max().item() <= ATOL
+    torch.cuda.synchronize()
+    for lf, lp in zip(fused.layers, plain.layers):
+        assert lf.pending is None and lf.n == lp.n == 30
+        assert torch.equal(lf.keys, lp.keys) and torch.equal(lf.values, lp.values)
+    # A splice after fused appends sees every row.
+    kv.splice(fused, Split(4, 9, 11), model.model.rotary_emb.inv_freq)
+    kv.splice(plain, Split(4, 9, 11), model.model.rotary_emb.inv_freq)
+    for lf, lp in zip(fused.layers, plain.layers):
+        assert torch.equal(lf.keys, lp.keys) and torch.equal(lf.values, lp.values)

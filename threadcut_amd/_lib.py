@@ -47,6 +47,8 @@ SIGNATURES = {
     "tc_decode_combine": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _I64P, _I, _P]),
     "tc_decode_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
                                  _P, _S, _P, _I64P, _P]),
+    "tc_decode_append_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I64, _I, _I, _I,
+                                        _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_shift_keys": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I64, _I, _I, _FP, _P]),
     "tc_splice_rope": (_I, [_PP, _PP, _I, _I64P, _I, _I, _I64, _I, _I, _I64, _I64, _I64, _FP, _P]),
     "tc_splice_copy": (_I, [_PP, _PP, _I64P, _I64, _PP, _PP, _I64P, _I, _I, _I, _I, _I, _I64, _I64, _I64,
@@ -94,6 +96,10 @@ def dtype_code(t):
 
 def i64x3(a, b, c):
     return (ctypes.c_int64 * 3)(int(a), int(b), int(c))
+
+
+def i64x2(a, b):
+    return (ctypes.c_int64 * 2)(int(a), int(b))
 
 
 def ptr_array(ptrs):

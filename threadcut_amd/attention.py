@@ -13,7 +13,8 @@ import torch.nn.functional as F
 from transformers import AttentionInterface
 from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 
-from .flash_decode import decode_into
+from . import kv
+from .flash_decode import decode_append_into, decode_into
 
 NAME = "threadcut"
 
@@ -39,8 +40,19 @@ def attention(module, query, key, value, attention_mask, dropout=0.0, scaling=No
     if q == 1 and attention_mask is None:
         # [b, 1, hq, d] contiguous is [b, hkv, g, d] with head index h*g + i.
         out = torch.empty((b, 1, hq, d), dtype=query.dtype, device=query.device)
-        decode_into(query.reshape(b, hkv, g, d), key, value, scaling, out.view(b, hkv, g, d))
+        layer = kv.take_pending(key)
+        if layer is not None:
+            # GrowingLayer deferred this token's append: write it and attend in one launch.
+            k_new, v_new = layer.pending
+            layer.pending = None
+            decode_append_into(query.reshape(b, hkv, g, d), layer.kbuf, layer.vbuf, k_new, v_new, layer.n,
+                               scaling, out.view(b, hkv, g, d))
+        else:
+            decode_into(query.reshape(b, hkv, g, d), key, value, scaling, out.view(b, hkv, g, d))
         return out, None
+    pending = kv.take_pending(key)
+    if pending is not None:  # a deferred append must land before SDPA reads the cache
+        pending.flush()
     is_causal = attention_mask is None and q > 1 and q == key.shape[2]
     out = F.scaled_dot_product_attention(query, repeat_kv(key, g), repeat_kv(value, g),
                                          attn_mask=attention_mask, scale=scaling, is_causal=is_causal)

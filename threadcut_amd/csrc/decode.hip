@@ -75,6 +75,14 @@ struct PartialArgs {
   int heads, group, splits, split_tokens;
   int interleave;      // 0: split s owns tokens [s*T, (s+1)*T); 1: 16-token tiles dealt round-robin
   float scale_log2;    // softmax scale * log2(e)
+  // Append (k_new != null): the cache holds n - 1 tokens and the new token's
+  // K/V rows [B, H, D] are attended from k_new/v_new and written to row n - 1
+  // of the cache (k_w/v_w) by wave 0 of split 0; no other wave reads that row.
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t skn_b, skn_h, svn_b, svn_h;
+  uint16_t* k_w;
+  uint16_t* v_w;
 };
 
 struct CombineArgs {
@@ -337,8 +345,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   const int h = blockIdx.y;
   const int b = blockIdx.z;
 
-  // Lengths past the buffer (or negative) are clamped into [0, n].
-  const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), a.n) : a.n;
+  // Lengths past the buffer (or negative) are clamped into [0, n]; with an
+  // append, the last of the n tokens comes from k_new/v_new, not the cache.
+  const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), a.n)
+                             : (a.k_new ? a.n - 1 : a.n);
   // The wave's 16-token tiles: first, first + stride, ... with tokens < end.
   // Contiguous: split s, wave w own [s*T + w*T/W, s*T + (w+1)*T/W). Interleaved:
   // all S*W waves of a head sweep the cache together, wave g taking tiles
@@ -408,6 +418,30 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
         }
       }
       if (done) break;
+    }
+  }
+
+  if (a.k_new && split == 0 && wave == 0) {
+    // The appended token, as a tile whose only row is slot 0 (the buffer range
+    // is one row, so the other slots read zero and are masked).
+    const char* kn = reinterpret_cast<const char*>(a.k_new + b * a.skn_b + h * a.skn_h);
+    const char* vn = reinterpret_cast<const char*>(a.v_new + b * a.svn_b + h * a.svn_h);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kn, kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vn, kHeadDim * 2);
+    Tile t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      t.k[j] = bload16(rk, koff[j]);
+      t.v[j] = bload16(rv, voff[j]);
+    }
+    st.step(t, qw, my_slot == 0, a.scale_log2);
+    if (lane < 32) {
+      const bool is_v = lane >= 16;
+      const int chunk = 8 * (lane & 15);
+      const uint16_t* src = is_v ? a.v_new + b * a.svn_b + h * a.svn_h : a.k_new + b * a.skn_b + h * a.skn_h;
+      uint16_t* dst = is_v ? a.v_w + b * a.sv_b + h * a.sv_h + len * a.sv_t
+                           : a.k_w + b * a.sk_b + h * a.sk_h + len * a.sk_t;
+      *reinterpret_cast<uint4*>(dst + chunk) = *reinterpret_cast<const uint4*>(src + chunk);
     }
   }
 
@@ -668,10 +702,21 @@ size_t tc_decode_workspace_bytes(int batch, int kv_heads, int group, int head_di
 namespace tc {
 namespace {
 
+// The new token of an append-and-attend call: K/V rows [B, H, D] and the
+// writable cache they go to.
+struct Append {
+  const void* k_new;
+  const int64_t* kn_strides;  // (batch, head)
+  const void* v_new;
+  const int64_t* vn_strides;
+  void* k_cache;
+  void* v_cache;
+};
+
 int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
                  const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens, int batch,
                  int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens, int num_splits,
-                 float* o_part_dev, float* lse_part_dev, int interleave, void* stream) {
+                 float* o_part_dev, float* lse_part_dev, int interleave, const Append* app, void* stream) {
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens == 0 && num_splits == 0) return TC_OK;  // empty caches: nothing to read
@@ -716,6 +761,14 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.splits = num_splits;
   a.split_tokens = split_tokens;
   a.interleave = interleave;
+  a.k_new = app ? static_cast<const uint16_t*>(app->k_new) : nullptr;
+  a.v_new = app ? static_cast<const uint16_t*>(app->v_new) : nullptr;
+  a.skn_b = app ? app->kn_strides[0] : 0;
+  a.skn_h = app ? app->kn_strides[1] : 0;
+  a.svn_b = app ? app->vn_strides[0] : 0;
+  a.svn_h = app ? app->vn_strides[1] : 0;
+  a.k_w = app ? static_cast<uint16_t*>(app->k_cache) : nullptr;
+  a.v_w = app ? static_cast<uint16_t*>(app->v_cache) : nullptr;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -735,7 +788,8 @@ int tc_decode_partial(const void* q_dev, const int64_t q_strides[3], const void*
                       int num_splits, float* o_part_dev, float* lse_part_dev, void* stream) {
   clear_error();
   return partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
-                      head_dim, dtype, scale, split_tokens, num_splits, o_part_dev, lse_part_dev, 0, stream);
+                      head_dim, dtype, scale, split_tokens, num_splits, o_part_dev, lse_part_dev, 0, nullptr,
+                      stream);
 }
 
 int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int batch, int kv_heads, int group,
@@ -771,12 +825,16 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   return hip_status(hipGetLastError(), "decode_combine launch");
 }
 
-int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
-                        const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
-                        int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
-                        void* workspace_dev, size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
-                        void* stream) {
-  clear_error();
+}  // extern "C"
+
+namespace tc {
+namespace {
+
+int attention_impl(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                   const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
+                   int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
+                   void* workspace_dev, size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
+                   const Append* app, void* stream) {
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
@@ -786,15 +844,51 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const voi
   if (S > 0 && (!workspace_dev || workspace_bytes < need))
     return fail(TC_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, need, S);
   float* o_part = static_cast<float*>(workspace_dev);
-  float* lse_part =
-      S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * group * head_dim : nullptr;
+  float* lse_part = S > 0 ? o_part + static_cast<size_t>(batch) * kv_heads * S * group * head_dim : nullptr;
   if (S > 0) {
     // Splits here are internal, so their tiles are dealt round-robin (the merged result is the same).
     rc = partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
-                      head_dim, dtype, scale, t, S, o_part, lse_part, TC_DECODE_INTERLEAVE, stream);
+                      head_dim, dtype, scale, t, S, o_part, lse_part, TC_DECODE_INTERLEAVE, app, stream);
     if (rc != TC_OK) return rc;
   }
   return tc_decode_combine(o_part, lse_part, batch, kv_heads, group, head_dim, S, out_dev, out_strides, dtype, stream);
+}
+
+}  // namespace
+}  // namespace tc
+
+extern "C" {
+
+int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                        const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
+                        int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
+                        void* workspace_dev, size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
+                        void* stream) {
+  clear_error();
+  return attention_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads,
+                        group, head_dim, dtype, scale, split_tokens, workspace_dev, workspace_bytes, out_dev,
+                        out_strides, nullptr, stream);
+}
+
+int tc_decode_append_attention(const void* q_dev, const int64_t q_strides[3], void* k_cache_dev,
+                               const int64_t k_strides[3], void* v_cache_dev, const int64_t v_strides[3],
+                               const void* k_new_dev, const int64_t k_new_strides[2], const void* v_new_dev,
+                               const int64_t v_new_strides[2], int64_t n_tokens, int batch, int kv_heads, int group,
+                               int head_dim, int dtype, float scale, int split_tokens, void* workspace_dev,
+                               size_t workspace_bytes, void* out_dev, const int64_t out_strides[3], void* stream) {
+  clear_error();
+  if (n_tokens < 1) return fail(TC_ERR_INVALID_ARGUMENT, "append needs n_tokens >= 1 (got %lld)", (long long)n_tokens);
+  if (!k_new_dev || !v_new_dev || !k_new_strides || !v_new_strides)
+    return fail(TC_ERR_INVALID_ARGUMENT, "null new-token K/V");
+  if (!aligned16(k_new_dev) || !aligned16(v_new_dev))
+    return fail(TC_ERR_ALIGNMENT, "new-token K/V not 16-byte aligned");
+  for (int i = 0; i < 2; ++i)
+    if (k_new_strides[i] < 0 || v_new_strides[i] < 0 || k_new_strides[i] % 8 || v_new_strides[i] % 8)
+      return fail(TC_ERR_ALIGNMENT, "new-token K/V strides must be non-negative multiples of 8");
+  const Append app{k_new_dev, k_new_strides, v_new_dev, v_new_strides, k_cache_dev, v_cache_dev};
+  return attention_impl(q_dev, q_strides, k_cache_dev, k_strides, v_cache_dev, v_strides, nullptr, n_tokens, batch,
+                        kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev, workspace_bytes, out_dev,
+                        out_strides, &app, stream);
 }
 
 }  // extern "C"

@@ -22,6 +22,25 @@ from .match import Split  # noqa: F401  (re-exported: the splice contract)
 
 HEAD_DIM = 128
 
+# Deferred single-token appends of GrowingLayers in fused-append mode, by the
+# address of the layer's K buffer; the "threadcut" attention takes them.
+_PENDING = {}
+
+
+def take_pending(key):
+    """The GrowingLayer whose deferred append `key` (a [..., :n, :] view) carries, or None.
+
+    Clears the registration; the caller must then write the new token itself
+    (flash_decode.decode_append_into does, inside the attention kernel).
+    """
+    if not key.is_cuda:
+        return None
+    layer = _PENDING.get(key.data_ptr())
+    if layer is None or layer.pending is None or key.shape[-2] != layer.n:
+        return None
+    del _PENDING[key.data_ptr()]
+    return layer
+
 
 def rotate_half(x):
     """cat(-x2, x1) over the two halves of the last dim (threadcut/kv.py:15-17)."""
@@ -110,6 +129,8 @@ def splice(cache, s, inv_freq):
     if all(isinstance(layer, GrowingLayer) for layer in cache.layers):
         live = [layer for layer in cache.layers if getattr(layer, "kbuf", None) is not None]
         for layer in live:
+            layer.flush()
+        for layer in live:
             if s.c0 + s.c > layer.n:
                 raise ValueError(f"splice: suffix [{s.c0}, {s.c0 + s.c}) past the {layer.n} cached tokens")
         if s.c and s.gap:
@@ -154,11 +175,28 @@ class GrowingLayer(DynamicLayer):
     Appending a token writes in place instead of re-copying the cache with
     torch.cat. Capacity grows by max(need, 1.25 * cap, cap + 2048) tokens.
     ``keys``/``values`` are views ``kbuf[..., :n, :]``.
+
+    With ``fused_append`` (for models run with the "threadcut" attention), a
+    single-token GPU update does not copy: the new rows stay pending and the
+    decode attention kernel writes them while it attends. Any other access
+    path (a later update, splice, crop) writes a pending row first.
     """
+
+    fused_append = False
+    pending = None
 
     def lazy_initialization(self, key_states, value_states):
         super().lazy_initialization(key_states, value_states)
         self.n, self.kbuf, self.vbuf = 0, None, None
+
+    def flush(self):
+        """Write a deferred append that no attention call consumed."""
+        if self.pending is not None:
+            _PENDING.pop(self.kbuf.data_ptr(), None)
+            k, v = self.pending
+            self.kbuf[..., self.n - 1:self.n, :] = k
+            self.vbuf[..., self.n - 1:self.n, :] = v
+            self.pending = None
 
     def _reserve(self, need, like):
         cap = 0 if self.kbuf is None else self.kbuf.shape[-2]
@@ -178,20 +216,27 @@ class GrowingLayer(DynamicLayer):
     def update(self, key_states, value_states, *args, **kwargs):
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
+        self.flush()
         add = key_states.shape[-2]
         self._reserve(self.n + add, key_states)
-        self.kbuf[..., self.n:self.n + add, :] = key_states
-        self.vbuf[..., self.n:self.n + add, :] = value_states
+        if self.fused_append and add == 1 and key_states.is_cuda:
+            self.pending = (key_states, value_states)
+            _PENDING[self.kbuf.data_ptr()] = self
+        else:
+            self.kbuf[..., self.n:self.n + add, :] = key_states
+            self.vbuf[..., self.n:self.n + add, :] = value_states
         self.n += add
         self._view()
         return self.keys, self.values
 
     def crop(self, max_length):
+        self.flush()
         self.n = min(self.n, max_length)
         self._view()
 
     def splice(self, s, inv_freq):
         """In-place A·B·C -> A·C: only C is touched, so a prune costs O(|C|)."""
+        self.flush()
         if s.c0 + s.c > self.n:
             raise ValueError(f"splice: suffix [{s.c0}, {s.c0 + s.c}) past the {self.n} cached tokens")
         if s.c and s.gap:
@@ -200,8 +245,14 @@ class GrowingLayer(DynamicLayer):
         self._view()
 
 
-def new_cache(config):
-    """A DynamicCache whose layers are GrowingLayers (threadcut/kv.py:95-98)."""
+def new_cache(config, fused_append=False):
+    """A DynamicCache whose layers are GrowingLayers (threadcut/kv.py:95-98).
+
+    fused_append=True defers single-token appends into the decode attention
+    kernel; use it only with the "threadcut" attention implementation.
+    """
     cache = DynamicCache(config=config)
     cache.layers = [GrowingLayer() for _ in cache.layers]
+    for layer in cache.layers:
+        layer.fused_append = fused_append
     return cache
