@@ -186,6 +186,19 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
                    int64_t a, int64_t c0, int64_t c,
                    const float* cos_sin_host, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Request split (host code, no GPU)                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Split(a, c0, c) of `fresh` against `cached` by the rule of
+ * threadcut/match.py:33-48 (longest common prefix capped at n_fresh - 1; the
+ * longest run of fresh[a:] that also starts in cached[a+1:] from a
+ * min_suffix-token anchor, first longest wins, capped at len(fresh[a:]) - 1;
+ * (a, a, 0) when suffix is 0 or too short). out = {a, c0, c}. The anchor
+ * search is a rolling hash, linear in n_cached plus the verified hits. */
+int tc_match_split(const int64_t* cached, int64_t n_cached, const int64_t* fresh, int64_t n_fresh,
+                   int64_t min_suffix, int suffix, int64_t out[3]);
+
 #ifdef __cplusplus
 }
 #endif

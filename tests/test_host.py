@@ -8,6 +8,7 @@ import pytest
 import torch
 from transformers import Qwen3Config
 
+from oracle import match as oracle_match
 from oracle import splice as osp
 from threadcut_amd import attention, flash_decode, kv, workloads
 from threadcut_amd.match import Split, lcp, split
@@ -24,20 +25,17 @@ def test_split_rule_known_answers():
 
 
 def brute_split(cached, new, min_suffix, suffix=True):
-    """The Split rule by exhaustive search (threadcut/match.py:33-48 semantics)."""
+    """The Split rule by exhaustive search: every start j > a and every run length
+    c in [min_suffix, len(rest) - 1] with cached[j:j+c] == rest[:c]; first longest wins."""
     a = min(lcp(cached, new), len(new) - 1)
-    rest = new[a:]
+    rest = new[a:] if a >= 0 else []
     best = Split(a, a, 0)
     if not suffix or len(rest) <= min_suffix or len(cached) - (a + 1) < min_suffix:
         return best
     for j in range(a + 1, len(cached) - min_suffix + 1):
-        if list(cached[j:j + min_suffix]) == list(rest[:min_suffix]):
-            c = 0
-            while j + c < len(cached) and c < len(rest) and cached[j + c] == rest[c]:
-                c += 1
-            c = min(c, len(rest) - 1)
-            if c > best.c:
-                best = Split(a, j, c)
+        runs = [c for c in range(min_suffix, len(rest)) if list(cached[j:j + c]) == list(rest[:c])]
+        if runs and max(runs) > best.c:
+            best = Split(a, j, max(runs))
     return best
 
 
@@ -51,7 +49,25 @@ def test_split_matches_exhaustive_search():
             i = rng.randrange(len(cached) // 2)
             new = cached[:i] + cached[i + rng.randrange(1, 4):] + [rng.randrange(vocab)]
         for ms, sfx in itertools.product((1, 2, 4), (True, False)):
-            assert split(cached, new, ms, sfx) == brute_split(cached, new, ms, sfx)
+            want = Split(*oracle_match.split(cached, new, ms, sfx))
+            assert split(cached, new, ms, sfx) == want
+            assert brute_split(cached, new, ms, sfx) == want
+
+
+def test_native_split_on_long_repetitive_caches():
+    """The rolling-hash matcher against the oracle where windows repeat and hashes collide often."""
+    rng = random.Random(1)
+    for _ in range(30):
+        period = rng.randrange(1, 6)
+        unit = [rng.randrange(3) for _ in range(period)]
+        cached = (unit * 400)[:rng.randrange(50, 1200)]
+        cut = rng.randrange(0, len(cached))
+        new = cached[:cut] + cached[cut + rng.randrange(1, 40):] + [7, 8]
+        for ms in (1, 3, 8):
+            assert split(cached, new, ms) == Split(*oracle_match.split(cached, new, ms))
+    big = list(range(200000))
+    s = split(big, big[:1000] + big[5000:150000], 32)
+    assert s == Split(1000, 5000, 144999)
 
 
 def test_lcp():

@@ -1,7 +1,8 @@
 """Build recipe of the threadcut HIP library (gfx950 only).
 
-Compiles every ``csrc/*.hip`` source with hipcc into ``_build/*.o`` (in
-parallel) and links ``libthreadcut_hip.so`` next to this file, where
+Compiles every ``csrc/*.hip`` source with hipcc (and the host-only
+``csrc/*.cpp`` with g++) into ``_build/*.o`` in parallel, and links
+``libthreadcut_hip.so`` next to this file, where
 ``threadcut_amd._lib`` loads it. Run as ``python -m threadcut_amd.build``.
 """
 import concurrent.futures
@@ -33,7 +34,10 @@ def hipcc():
 
 
 def _compile(src, obj):
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):  # host-only C++
+        cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", "-c", src, "-o", obj]
+    else:
+        cmd = [hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass reports the device-only feature flag as unknown; drop that noise.
     noise = "'-packed-fp32-ops' is not a recognized feature"
@@ -46,8 +50,8 @@ def _compile(src, obj):
 def build(verbose=False):
     """Compile and link the library; returns its path. Always rebuilds."""
     os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    objs = [os.path.join(BUILD, os.path.basename(s)[:-4] + ".o") for s in sources]
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
+    objs = [os.path.join(BUILD, os.path.splitext(os.path.basename(s))[0] + ".o") for s in sources]
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         for src, warn in zip(sources, ex.map(_compile, sources, objs)):
             if warn and verbose:

@@ -8,8 +8,10 @@ A is the longest common prefix (capped so D keeps at least one token), B the
 span the agent pruned, C the longest run of the new tokens after A that also
 appears in the cache after A (found from a ``min_suffix``-token anchor), and D
 the rest, the only part the model runs. ``Split(a, c0, c)`` feeds
-``kv.splice``. Host-side integer work, unchanged in meaning.
+``kv.splice``. Host-side integer work, unchanged in meaning; the search runs
+in the library's C++ matcher.
 """
+import ctypes
 from dataclasses import dataclass
 
 import numpy as np
@@ -37,22 +39,18 @@ def lcp(x, y):
 
 
 def split(cached, new, min_suffix=32, suffix=True):
-    """Split `new` against `cached` (threadcut/match.py:33-48)."""
-    a = min(lcp(cached, new), len(new) - 1)
-    rest = new[a:]
-    no_reuse = Split(a, a, 0)
-    if not suffix or len(rest) <= min_suffix or len(cached) - (a + 1) < min_suffix:
-        return no_reuse
-    hay = np.asarray(cached[a + 1:])
-    anchor = np.asarray(rest[:min_suffix])
-    n_starts = len(hay) - min_suffix + 1
-    hit = np.ones(n_starts, dtype=bool)
-    for i, tok in enumerate(anchor):  # anchor token i must sit at start + i
-        hit &= hay[i:i + n_starts] == tok
-    best = no_reuse
-    for off in np.flatnonzero(hit):
-        j = a + 1 + int(off)
-        c = min(lcp(cached[j:], rest), len(rest) - 1)
-        if c > best.c:
-            best = Split(a, j, c)
-    return best
+    """Split `new` against `cached` (threadcut/match.py:33-48).
+
+    Runs the native matcher (``tc_match_split``: rolling-hash anchor search,
+    linear in the cache length); token ids are taken as 64-bit integers.
+    """
+    from . import _lib
+
+    c = np.ascontiguousarray(np.asarray(cached, dtype=np.int64).reshape(-1))
+    n = np.ascontiguousarray(np.asarray(new, dtype=np.int64).reshape(-1))
+    out = (ctypes.c_int64 * 3)()
+    p64 = ctypes.POINTER(ctypes.c_int64)
+    rc = _lib.load().tc_match_split(c.ctypes.data_as(p64), len(c), n.ctypes.data_as(p64), len(n),
+                                    int(min_suffix), int(bool(suffix)), out)
+    _lib.check(rc, "tc_match_split")
+    return Split(int(out[0]), int(out[1]), int(out[2]))
