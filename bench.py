@@ -286,6 +286,33 @@ def measure_append(dev, n, steps):
             "us_per_layer_fused_append": round(ms_fused * 1e3 / LAYERS, 3)}
 
 
+def measure_match(seconds=2.0):
+    """Request split at a 131072-token cache: the native matcher vs the reference's numpy windows."""
+    import numpy as np
+
+    from oracle.match import split_windows
+    from threadcut_amd.match import split
+
+    rng = np.random.default_rng(6)
+    cached = rng.integers(0, 151936, 131072).astype(np.int64)
+    new = np.concatenate((cached[:20000], cached[60000:], rng.integers(0, 151936, 100)))
+
+    def timed(fn):
+        times, t_end = [], time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            r = fn(cached, new, 32)
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        return times[len(times) // 2], r
+
+    t_native, r_native = timed(split)
+    t_numpy, r_numpy = timed(split_windows)
+    assert tuple(r_native.__dict__.values()) == tuple(r_numpy), (r_native, r_numpy)
+    return {"cached_tokens": len(cached), "split": [r_native.a, r_native.c0, r_native.c],
+            "native_us": round(t_native * 1e6, 1), "reference_numpy_us": round(t_numpy * 1e6, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -374,6 +401,7 @@ def main():
         line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
         line["long_131072"] = {f"B{b}": measure_long(dev, b, max(10, args.steps // 10)) for b in (1, 4)}
         line["decode_append"] = measure_append(dev, n, max(20, args.steps // 4))
+        line["match_split"] = measure_match()
     if not args.no_splice:
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:

@@ -32,3 +32,31 @@ def split(cached, new, min_suffix=32, suffix=True):
             if c > best[2]:
                 best = (a, j, c)
     return best
+
+
+def split_windows(cached, new, min_suffix=32, suffix=True):
+    """threadcut/match.py:33-48 as the reference computes it: numpy sliding windows
+    over cached[a+1:] compared with the anchor, then lcp per hit. Used to time the
+    reference's CPU path next to the native matcher."""
+    import numpy as np
+
+    def np_lcp(x, y):
+        n = min(len(x), len(y))
+        if n == 0:
+            return 0
+        diff = np.flatnonzero(np.asarray(x[:n]) != np.asarray(y[:n]))
+        return int(diff[0]) if len(diff) else n
+
+    a = min(np_lcp(cached, new), len(new) - 1)
+    rest = new[a:]
+    if not suffix or len(rest) <= min_suffix or len(cached) - (a + 1) < min_suffix:
+        return (a, a, 0)
+    arr = np.asarray(cached)
+    windows = np.lib.stride_tricks.sliding_window_view(arr[a + 1:], min_suffix)
+    hits = np.flatnonzero((windows == np.asarray(rest[:min_suffix])).all(axis=1)) + a + 1
+    best = (a, a, 0)
+    for j in hits:
+        c = min(np_lcp(cached[j:], rest), len(rest) - 1)
+        if c > best[2]:
+            best = (a, int(j), c)
+    return best

@@ -52,6 +52,7 @@ def test_split_matches_exhaustive_search():
             want = Split(*oracle_match.split(cached, new, ms, sfx))
             assert split(cached, new, ms, sfx) == want
             assert brute_split(cached, new, ms, sfx) == want
+            assert Split(*oracle_match.split_windows(cached, new, ms, sfx)) == want
 
 
 def test_native_split_on_long_repetitive_caches():
