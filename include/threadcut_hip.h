@@ -187,6 +187,33 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
                    const float* cos_sin_host, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Prefill attention                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* The prefill branch of threadcut/attention.py:43-46 without expanding the
+ * KV heads (repeat_kv, attention.py:25-27): for query token t of every
+ * query head hq = h*g + i (g = q_heads / kv_heads),
+ *   out[b, t, hq, :] = softmax_j(q[b, hq, t]·k[b, h, j]ᵀ·scale + mask)·v[b, h, j]
+ * over keys j < n_tokens, fp32 softmax and accumulation. The query tokens sit
+ * at positions n_tokens - q_len + t. Masking is one of
+ *   - mask_dev != NULL: boolean [mb, q_len, n_tokens] bytes (1 = attend),
+ *     strides mask_strides (batch stride 0 broadcasts); causal must be 0;
+ *   - causal != 0: key j visible to token t iff j <= n_tokens - q_len + t
+ *     (SDPA's is_causal when q_len == n_tokens);
+ *   - neither: every key visible.
+ * A query row with no visible key gets zeros. q [b, hq, q_len, d] and k/v
+ * [b, hkv, n_tokens, d] with element strides {batch, head, token} and a
+ * contiguous last dim; out [b, q_len, hq, d] with strides {batch, token,
+ * head}. head_dim must be 128, g one of 1, 2, 4, 8. */
+int tc_prefill_attention(const void* q, const int64_t q_strides[3],
+                         const void* k, const int64_t k_strides[3],
+                         const void* v, const int64_t v_strides[3],
+                         const uint8_t* mask, const int64_t mask_strides[3], int causal,
+                         int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
+                         int head_dim, int dtype, float scale,
+                         void* out, const int64_t out_strides[3], void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Request split (host code, no GPU)                                         */
 /* ------------------------------------------------------------------------ */
 

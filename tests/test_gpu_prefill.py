@@ -1,0 +1,159 @@
+"""Prefill parity on the GPU: the GQA-native HIP kernel vs the float64 oracle of
+threadcut/attention.py:43-47 and vs the reference's own GPU route (repeat_kv +
+torch SDPA) on the same seeded inputs.
+
+Tolerance: max-abs 2e-3 for fp16 (the north-star attention bar); bf16 outputs
+round to 8 bits, so bf16 gets 1.6e-2, and in every case the kernel's error
+against float64 must not exceed 1.5x that of torch SDPA on the expanded K/V.
+"""
+import numpy as np
+import pytest
+import torch
+from transformers.masking_utils import sdpa_mask
+
+from oracle import prefill as op
+from threadcut_amd import _lib, attention, prefill, workloads
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+SCALE = 128 ** -0.5
+
+
+def ref64(q, k, v, mask=None, causal=False, scale=SCALE):
+    m = None if mask is None else mask.cpu().numpy()
+    return op.prefill_f64(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), scale,
+                          mask=m, causal=causal)
+
+
+def torch_route(q, k, v, mask, causal, scale=SCALE):
+    """The reference's prefill on the GPU: expanded K/V and SDPA in the input dtype."""
+    g = q.shape[1] // k.shape[1]
+    out = torch.nn.functional.scaled_dot_product_attention(
+        q, attention.repeat_kv(k, g), attention.repeat_kv(v, g), attn_mask=mask, scale=scale, is_causal=causal)
+    return out.transpose(1, 2)
+
+
+def check(q, k, v, mask=None, causal=False, scale=SCALE, label=""):
+    print(f"case: {label} q={tuple(q.shape)} k={tuple(k.shape)} dtype={q.dtype} causal={causal} "
+          f"mask={None if mask is None else tuple(mask.shape)}", flush=True)
+    out = prefill.prefill_attention(q, k, v, mask, scale, causal)
+    torch.cuda.synchronize()
+    assert out.shape == (q.shape[0], q.shape[2], q.shape[1], q.shape[3]) and out.is_contiguous()
+    want = ref64(q, k, v, mask, causal, scale)
+    err = np.abs(out.float().cpu().numpy() - want).max()
+    tref = torch_route(q, k, v, mask, causal, scale)
+    terr = np.abs(tref.float().cpu().numpy() - want).max()
+    assert err <= max(TOL[q.dtype], 1.5 * terr), (err, terr)
+    return out
+
+
+@pytest.mark.parametrize("g", [1, 2, 4, 8])
+@pytest.mark.parametrize("n", [2, 3, 16, 17, 63, 64, 65, 130, 300])
+def test_causal_full_prompt(gpu, g, n):
+    """q == n, no mask: SDPA's is_causal."""
+    q_heads, kv_heads = {1: (8, 8), 2: (16, 8), 4: (32, 8), 8: (16, 2)}[g]
+    q, k, v = workloads.prefill_inputs(10 * g + n, q_len=n, n=n, q_heads=q_heads, kv_heads=kv_heads, device=gpu)
+    check(q, k, v, causal=True, label=f"causal g={g}")
+
+
+@pytest.mark.parametrize("q_len,past", [(1, 5), (2, 1), (5, 60), (37, 100), (64, 64), (65, 200), (300, 1000)])
+def test_chunk_on_top_of_a_cache(gpu, q_len, past):
+    """The engine's chunked prefill: the boolean mask sdpa_mask builds for queries at past.."""
+    n = past + q_len
+    q, k, v = workloads.prefill_inputs(q_len + past, q_len=q_len, n=n, device=gpu)
+    mask = sdpa_mask(batch_size=1, q_length=q_len, kv_length=n, q_offset=past, device=gpu)
+    if mask is None:  # q_len == 1 without padding: every key visible
+        mask = torch.ones((1, 1, q_len, n), dtype=torch.bool, device=gpu)
+    assert torch.equal(mask.cpu(), workloads.causal_mask(q_len, n))
+    check(q, k, v, mask=mask, label="chunk")
+
+
+@pytest.mark.parametrize("q_len,n", [(2, 2), (7, 50), (100, 333)])
+def test_no_mask_attends_to_everything(gpu, q_len, n):
+    q, k, v = workloads.prefill_inputs(q_len * n, q_len=q_len, n=n, device=gpu)
+    check(q, k, v, label="full")
+
+
+@pytest.mark.parametrize("batch_mask", [1, 3])
+def test_random_masks_and_batches(gpu, batch_mask):
+    b, L, n = 3, 70, 150
+    q, k, v = workloads.prefill_inputs(5, batch=b, q_len=L, n=n, device=gpu)
+    g = torch.Generator().manual_seed(batch_mask)
+    m = torch.rand((batch_mask, 1, L, n), generator=g) < 0.3
+    m[..., 7] = True
+    check(q, k, v, mask=m.to(gpu), label=f"random mask batch {batch_mask}")
+
+
+def test_rows_without_visible_keys_are_zero(gpu):
+    q, k, v = workloads.prefill_inputs(6, q_len=20, n=40, device=gpu)
+    m = workloads.causal_mask(20, 40).clone()
+    m[..., 5, :] = False
+    m[..., 11, :] = False
+    out = check(q, k, v, mask=m.to(gpu), label="empty rows")
+    assert torch.all(out[0, 5] == 0) and torch.all(out[0, 11] == 0)
+
+
+def test_bf16(gpu):
+    q, k, v = workloads.prefill_inputs(8, q_len=150, n=400, dtype=torch.bfloat16, device=gpu)
+    check(q, k, v, mask=workloads.causal_mask(150, 400).to(gpu), label="bf16 chunk")
+    q, k, v = workloads.prefill_inputs(9, q_len=130, n=130, dtype=torch.bfloat16, device=gpu)
+    check(q, k, v, causal=True, label="bf16 causal")
+
+
+def test_strided_cache_views_and_scales(gpu):
+    """K/V as views [.., :n, :] of larger buffers (the GrowingLayer layout), contiguous query, big scale."""
+    q, k, v = workloads.prefill_inputs(11, q_len=90, n=90, device=gpu)
+    kb = torch.zeros((1, 8, 256, 128), dtype=k.dtype, device=gpu)
+    vb = torch.full((1, 8, 256, 128), float("nan"), dtype=k.dtype, device=gpu)
+    kb[:, :, :90] = k
+    vb[:, :, :90] = v
+    check(q.contiguous(), kb[:, :, :90], vb[:, :, :90], causal=True, label="cache views")
+    check(q, k, v, causal=True, scale=1.0, label="scale 1")
+    check(q * 4, k, v, causal=True, scale=1.0, label="large scores")
+
+
+def test_through_attention_interface(gpu):
+    """attention.attention() takes the kernel for both prefill masks the model produces."""
+    q, k, v = workloads.prefill_inputs(12, q_len=96, n=96, device=gpu)
+    out, w = attention.attention(None, q, k, v, None, scaling=SCALE)
+    assert w is None
+    assert np.abs(out.float().cpu().numpy() - ref64(q, k, v, causal=True)).max() <= TOL[q.dtype]
+    q, k, v = workloads.prefill_inputs(13, q_len=96, n=250, device=gpu)
+    mask = sdpa_mask(batch_size=1, q_length=96, kv_length=250, q_offset=154, device=gpu)
+    out, _ = attention.attention(None, q, k, v, mask, scaling=SCALE)
+    assert np.abs(out.float().cpu().numpy() - ref64(q, k, v, mask)).max() <= TOL[q.dtype]
+
+
+def test_workload_shape_vs_torch_route(gpu):
+    """One 2048-token chunk on top of the 7716 tokens the splice keeps (32/8 heads): within
+    tolerance of the reference's GPU route computed in fp32."""
+    q, k, v = workloads.prefill_inputs(14, device=gpu)
+    L, n = q.shape[2], k.shape[2]
+    mask = workloads.causal_mask(L, n, device=gpu)
+    print(f"case: workload chunk q={L} n={n}", flush=True)
+    out = prefill.prefill_attention(q, k, v, mask, SCALE)
+    outs = [torch_route(q[:, 8 * i:8 * i + 8].float(), k[:, 2 * i:2 * i + 2].float(),
+                        v[:, 2 * i:2 * i + 2].float(), mask, False) for i in range(4)]
+    ref = torch.cat(outs, 2)
+    torch.cuda.synchronize()
+    assert (out.float() - ref).abs().max().item() <= TOL[q.dtype]
+
+
+def test_rejects(gpu):
+    q, k, v = workloads.prefill_inputs(15, q_len=8, n=8, q_heads=12, kv_heads=4, device=gpu)
+    assert not prefill.supports(q, k, None)
+    with pytest.raises(RuntimeError, match="group 3"):
+        prefill.prefill_attention(q, k, v, None, SCALE, True)
+    q, k, v = workloads.prefill_inputs(15, q_len=8, n=8, device=gpu)
+    with pytest.raises(ValueError, match="either"):
+        prefill.prefill_attention(q, k, v, workloads.causal_mask(8, 8).to(gpu), SCALE, True)
+    with pytest.raises(ValueError, match="bool"):
+        prefill.prefill_attention(q, k, v, torch.zeros((1, 1, 8, 8), device=gpu), SCALE)
+    assert not prefill.supports(q, k, torch.zeros((1, 1, 8, 8), device=gpu))
+    with pytest.raises(RuntimeError, match="q_len"):
+        lib = _lib.load()
+        rc = lib.tc_prefill_attention(q.data_ptr(), _lib.i64x3(0, 0, 0), k.data_ptr(), _lib.i64x3(0, 0, 128),
+                                      v.data_ptr(), _lib.i64x3(0, 0, 128), None, None, 1, 9, 8, 1, 32, 8, 128, 0,
+                                      SCALE, q.data_ptr(), _lib.i64x3(0, 0, 0), None)
+        _lib.check(rc, "tc_prefill_attention")

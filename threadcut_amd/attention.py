@@ -4,16 +4,18 @@ Drop-in for threadcut/attention.py:22-51. Decode (one query token, no mask):
 the g query heads sharing a KV head are handed to the split-KV HIP kernels of
 ``flash_decode`` together with the unexpanded cache views, for any batch
 size (the reference used its GPU kernel for b == 1 and SDPA otherwise; both
-compute the same softmax). Prefill keeps the reference's path: expand KV once
-and run SDPA with the mask (threadcut/attention.py:43-46); it is not part of
-the decode hot path.
+compute the same softmax). Prefill (threadcut/attention.py:43-46) runs the
+GQA-native HIP kernel of ``prefill`` on the unexpanded K/V for GPU tensors
+with head_dim 128, g in (1, 2, 4, 8) and no mask or a boolean [b|1, 1, q, n]
+mask (what the registered ``sdpa_mask`` produces). Other calls, host tensors
+included, keep the reference's own path: expand KV once and run SDPA.
 """
 import torch
 import torch.nn.functional as F
 from transformers import AttentionInterface
 from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 
-from . import kv
+from . import kv, prefill
 from .flash_decode import decode_append_into, decode_into
 
 NAME = "threadcut"
@@ -54,6 +56,8 @@ def attention(module, query, key, value, attention_mask, dropout=0.0, scaling=No
     if pending is not None:  # a deferred append must land before SDPA reads the cache
         pending.flush()
     is_causal = attention_mask is None and q > 1 and q == key.shape[2]
+    if prefill.supports(query, key, attention_mask):
+        return prefill.prefill_attention(query, key, value, attention_mask, scaling, is_causal), None
     out = F.scaled_dot_product_attention(query, repeat_kv(key, g), repeat_kv(value, g),
                                          attn_mask=attention_mask, scale=scaling, is_causal=is_causal)
     return out.transpose(1, 2).contiguous(), None

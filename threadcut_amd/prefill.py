@@ -1,0 +1,88 @@
+"""GQA-native prefill attention on MI355X.
+
+Drop-in for the prefill branch of threadcut/attention.py:43-46, which expands
+every KV head g = Hq/Hkv times (``repeat_kv``, attention.py:25-27) and runs
+SDPA with the boolean mask or ``is_causal``. ``tc_prefill_attention`` reads
+the unexpanded K/V instead: a work-group owns 64 query rows of one KV head
+(64/g tokens × its g query heads), stages each 64-key tile of K and V in LDS
+once for all of them and runs QKᵀ and PV on the matrix cores with an fp32
+online softmax. This module checks tensors and passes pointers, strides and
+the current stream.
+"""
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+GROUPS = (1, 2, 4, 8)
+
+
+def supports(query, key, attention_mask):
+    """True if ``prefill_attention`` takes this call: a GPU call with head_dim 128,
+    g in (1, 2, 4, 8) and no mask or a boolean mask [b|1, 1, q, n]."""
+    b, hq, q, d = query.shape
+    hkv = key.shape[1]
+    if not query.is_cuda or d != HEAD_DIM or hq % hkv or hq // hkv not in GROUPS:
+        return False
+    if attention_mask is None:
+        return True
+    m = attention_mask
+    return (m.dtype == torch.bool and m.dim() == 4 and m.shape[0] in (1, b) and m.shape[1] == 1
+            and tuple(m.shape[2:]) == (q, key.shape[2]) and m.device == query.device)
+
+
+def _strides(t, dims, token_dim=None):
+    """Element strides of `dims`; size-1 dims get stride 0 (never stepped), except
+    a size-1 token dim of K/V, which gets the row length."""
+    st = [t.stride(i) if t.shape[i] > 1 else 0 for i in dims]
+    if token_dim is not None and t.shape[token_dim] <= 1:
+        st[dims.index(token_dim)] = t.shape[-1]
+    return _lib.i64x3(*st)
+
+
+def prefill_attention(query, key, value, attention_mask=None, scale=None, is_causal=False, out=None):
+    """SDPA(query, repeat_kv(key, g), repeat_kv(value, g), attention_mask, scale,
+    is_causal).transpose(1, 2) without expanding K/V.
+
+    query [b, hq, q, d], key/value [b, hkv, n, d] (any strides, contiguous last
+    dim), attention_mask None or bool [b|1, 1, q, n] (True = attend).
+    ``is_causal`` needs no mask and aligns the queries to the end of the keys
+    (identical to SDPA's when q == n). Returns out [b, q, hq, d] (a new
+    contiguous tensor unless `out` is given). Rows with no visible key are 0.
+    """
+    _lib.require_gpu(query, key, value, what="prefill_attention")
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        raise ValueError("prefill_attention: expected query [b,hq,q,d], key/value [b,hkv,n,d]")
+    if not (query.dtype == key.dtype == value.dtype):
+        raise TypeError(f"prefill_attention: dtypes differ ({query.dtype}, {key.dtype}, {value.dtype})")
+    b, hq, q, d = query.shape
+    hkv, n = key.shape[1], key.shape[2]
+    if key.shape != value.shape or key.shape[0] != b or key.shape[3] != d:
+        raise ValueError(f"prefill_attention: shapes query {tuple(query.shape)}, key {tuple(key.shape)}, "
+                         f"value {tuple(value.shape)} disagree")
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.stride(3) != 1:
+            raise ValueError(f"prefill_attention: {name} must have a contiguous last dimension")
+    if attention_mask is not None and is_causal:
+        raise ValueError("prefill_attention: pass either attention_mask or is_causal")
+    if out is None:
+        out = torch.empty((b, q, hq, d), dtype=query.dtype, device=query.device)
+    elif out.shape != (b, q, hq, d) or out.dtype != query.dtype or out.device != query.device or out.stride(3) != 1:
+        raise ValueError("prefill_attention: out must be [b, q, hq, d] in query's dtype and device")
+    mask_ptr, mask_strides = None, None
+    if attention_mask is not None:
+        m = attention_mask
+        if m.dtype != torch.bool or m.dim() != 4 or m.shape[1] != 1 or m.shape[0] not in (1, b) \
+                or tuple(m.shape[2:]) != (q, n) or m.device != query.device:
+            raise ValueError(f"prefill_attention: attention_mask must be bool [b|1, 1, {q}, {n}] on the device")
+        m = m[:, 0]
+        mask_ptr, mask_strides = m.data_ptr(), _strides(m, (0, 1, 2))
+    scale = scale if scale is not None else d ** -0.5
+    lib = _lib.load()
+    rc = lib.tc_prefill_attention(
+        query.data_ptr(), _strides(query, (0, 1, 2)), key.data_ptr(), _strides(key, (0, 1, 2), 2),
+        value.data_ptr(), _strides(value, (0, 1, 2), 2), mask_ptr, mask_strides, int(bool(is_causal)),
+        q, n, b, hq, hkv, d, _lib.dtype_code(query.dtype), float(scale),
+        out.data_ptr(), _strides(out, (0, 1, 2)), _lib.stream_of(query.device))
+    _lib.check(rc, "tc_prefill_attention")
+    return out

@@ -62,3 +62,28 @@ def layer_caches(seed, layers, n, kv_heads=8, head_dim=128, batch=1, dtype=torch
 def inv_freq(theta=1e6, head_dim=128):
     """transformers' default RoPE inverse frequencies, float32 [head_dim / 2]."""
     return (1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))).float()
+
+
+# Prefill: the engine runs new tokens in chunks of 2048 (threadcut/engine.py:46-48).
+# After SPLICE_SPLIT the cache keeps a + c = 7716 tokens; the next chunk attends to them.
+PREFILL_CHUNK = 2048
+PREFILL_PAST = SPLICE_SPLIT.a + SPLICE_SPLIT.c
+
+
+def prefill_inputs(seed, batch=1, q_len=PREFILL_CHUNK, n=PREFILL_PAST + PREFILL_CHUNK, q_heads=32, kv_heads=8,
+                   head_dim=128, dtype=torch.float16, device="cpu"):
+    """(query [B, Hq, q_len, D] as the transposed view of [B, q_len, Hq, D] that
+    transformers hands over, key [B, Hkv, n, D], value)."""
+    g = _gen(seed, device)
+    q = randn((batch, q_len, q_heads, head_dim), g, dtype, device).transpose(1, 2)
+    k = randn((batch, kv_heads, n, head_dim), g, dtype, device)
+    v = randn((batch, kv_heads, n, head_dim), g, dtype, device)
+    return q, k, v
+
+
+def causal_mask(q_len, n, batch=1, device="cpu"):
+    """Boolean [B, 1, q_len, n]: query t (at position n - q_len + t) sees keys <= its position,
+    the mask transformers' sdpa_mask builds for a chunk on top of a cache."""
+    t = torch.arange(q_len, device=device)[:, None] + (n - q_len)
+    m = torch.arange(n, device=device)[None, :] <= t
+    return m[None, None].expand(batch, 1, q_len, n)
