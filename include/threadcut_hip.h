@@ -196,8 +196,12 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
  *   out[b, t, hq, :] = softmax_j(q[b, hq, t]·k[b, h, j]ᵀ·scale + mask)·v[b, h, j]
  * over keys j < n_tokens, fp32 softmax and accumulation. The query tokens sit
  * at positions n_tokens - q_len + t. Masking is one of
- *   - mask_dev != NULL: boolean [mb, q_len, n_tokens] bytes (1 = attend),
- *     strides mask_strides (batch stride 0 broadcasts); causal must be 0;
+ *   - mask != NULL: boolean [mb, q_len, n_tokens] bytes (1 = attend) with
+ *     element strides mask_strides (batch stride 0 broadcasts one mask over
+ *     the batch); causal must be 0. mask_tiles, if not NULL, is the map
+ *     tc_prefill_mask_tiles built for this mask and these sizes (it lets the
+ *     kernel skip fully masked 64-key tiles and test no element of fully
+ *     visible ones); NULL tests every element;
  *   - causal != 0: key j visible to token t iff j <= n_tokens - q_len + t
  *     (SDPA's is_causal when q_len == n_tokens);
  *   - neither: every key visible.
@@ -208,10 +212,24 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
 int tc_prefill_attention(const void* q, const int64_t q_strides[3],
                          const void* k, const int64_t k_strides[3],
                          const void* v, const int64_t v_strides[3],
-                         const uint8_t* mask, const int64_t mask_strides[3], int causal,
+                         const uint8_t* mask, const int64_t mask_strides[3],
+                         const uint8_t* mask_tiles, size_t mask_tiles_bytes, int causal,
                          int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
                          int head_dim, int dtype, float scale,
                          void* out, const int64_t out_strides[3], void* stream);
+
+/* Bytes of the tile map of a mask with mask_batch distinct batch entries
+ * (1 for a broadcast mask); 0 for invalid sizes. */
+size_t tc_prefill_tiles_bytes(int64_t q_len, int64_t n_tokens, int mask_batch, int q_heads, int kv_heads);
+
+/* Classifies every (query block of 128/g tokens, 64-key tile) of a boolean
+ * mask as skip / full / mixed into `tiles` for tc_prefill_attention. One
+ * read of the mask; the map stays valid while the mask is unchanged, so the
+ * layers of one forward pass share it. Part of the prefill branch above
+ * (threadcut/attention.py:43-46); the reference has no separate step. */
+int tc_prefill_mask_tiles(const uint8_t* mask, const int64_t mask_strides[3], int mask_batch,
+                          int64_t q_len, int64_t n_tokens, int q_heads, int kv_heads,
+                          uint8_t* tiles, size_t tiles_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Request split (host code, no GPU)                                         */

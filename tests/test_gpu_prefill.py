@@ -154,6 +154,7 @@ def test_rejects(gpu):
     with pytest.raises(RuntimeError, match="q_len"):
         lib = _lib.load()
         rc = lib.tc_prefill_attention(q.data_ptr(), _lib.i64x3(0, 0, 0), k.data_ptr(), _lib.i64x3(0, 0, 128),
-                                      v.data_ptr(), _lib.i64x3(0, 0, 128), None, None, 1, 9, 8, 1, 32, 8, 128, 0,
+                                      v.data_ptr(), _lib.i64x3(0, 0, 128), None, None, None, 0, 1, 9, 8, 1, 32, 8,
+                                      128, 0,
                                       SCALE, q.data_ptr(), _lib.i64x3(0, 0, 0), None)
         _lib.check(rc, "tc_prefill_attention")

@@ -4,20 +4,31 @@
 // SDPA of q [b, hq, L, d] against repeat_kv(k), repeat_kv(v) (each KV head
 // expanded g = hq/hkv times) with the boolean attention mask, or is_causal
 // when there is no mask and L == n; output transposed to [b, L, hq, d].
-// Here the KV heads are never expanded: a work-group owns 64 query rows that
+// Here the KV heads are never expanded: a work-group owns 128 query rows that
 // are (query token, query head of the group) pairs of ONE KV head, so every
-// K/V tile it stages in LDS is read from HBM once and shared by the g heads.
+// K/V tile it stages in LDS is read once and shared by the g heads.
 //
-// Per 64-key tile, each wave (16 query rows) computes
-//   S^T = K . Q^T   with v_mfma_f32_16x16x32_f16: A = K rows from LDS, B = Q^T
-//                   from registers; lane l then holds keys 4(l/16)+r of query
-//                   row l%16, so a row's softmax needs only 4 lanes;
-//   O^T += V^T . P^T with P^T fed straight from those registers (fp16) and
-//                   V^T from LDS (V is transposed while staged), so no
-//                   cross-lane shuffle of P is needed.
-// The online softmax (max, sum, rescale) runs per query row in fp32, log2
-// domain. Tiles are double-buffered: the next tile's global loads are in
+// Per 64-key tile, each wave (32 query rows) computes
+//   S^T = K . Q^T   with v_mfma_f32_32x32x16: A = K rows from LDS, B = Q^T
+//                   from registers; lane l then holds 16 of the 32 keys of
+//                   each 32-key half for query row l%32 (the other 16 sit in
+//                   lane l^32), so a row's max and sum need one lane swap;
+//   O^T += V^T . P^T with P^T fed straight from those registers (fp16/bf16)
+//                   and V^T from LDS (V is transposed while staged), so P
+//                   never moves between lanes.
+// The online softmax runs per query row in fp32, log2 domain, as
+// p = exp2(s * c - m) with c = |scale| * log2(e) (a negative scale flips the
+// sign bits of Q instead). The accumulators are rescaled only when some
+// row's maximum moved.
+//
+// Every tile is classified for the whole work-group: SKIP (no row sees any
+// of its keys: not loaded), FULL (every row sees every key: no per-element
+// test) or MIXED (per-element test). Without a mask the class follows from
+// n and the causal diagonal; with a boolean mask it is read from a map that
+// tc_prefill_mask_tiles builds in one pass over the mask, once per mask.
+// Tiles are double-buffered: the next active tile's global loads are in
 // flight while the current one is multiplied.
+#include <algorithm>
 #include <cmath>
 
 #include "tc_common.hpp"
@@ -26,47 +37,71 @@ namespace tc {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kRows = 64;          // query rows per work-group (4 waves x 16)
+constexpr int kRows = 128;         // query rows per work-group (4 waves x 32)
 constexpr int kKeys = 64;          // keys per tile
 constexpr int kKStride = 136;      // halfs per K row in LDS (256 B + 16 B pad)
 constexpr int kVStride = 68;       // halfs per V^T row in LDS (128 B + 8 B pad)
 constexpr int kKTile = kKeys * kKStride;
 constexpr int kVTile = kHeadDim * kVStride;
 
+enum : int { TILE_SKIP = 0, TILE_FULL = 1, TILE_MIXED = 2 };
+
+// Waves per SIMD the register allocation targets: 2 leaves 256 registers a
+// lane and matches the two 68 KB work-groups the LDS of a CU holds.
+#ifndef TC_PREFILL_WAVES
+#define TC_PREFILL_WAVES 2
+#endif
+
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
-  const uint8_t* mask;      // null, or [mb, L, n] booleans (batch stride 0 broadcasts)
+  const uint8_t* mask;      // null, or [mb, L, n] booleans, keys contiguous (batch stride 0 broadcasts)
+  const uint8_t* tiles;     // null, or the tile classes of `mask` [mb][nblk][ntiles]
   uint16_t* out;            // [b, L, hq, d]
   int64_t sq_b, sq_h, sq_t;
   int64_t sk_b, sk_h, sk_t;
   int64_t sv_b, sv_h, sv_t;
-  int64_t sm_b, sm_q, sm_k;
+  int64_t sm_b, sm_q;
   int64_t so_b, so_t, so_h;
   int64_t q_len, n;         // query tokens, keys (the queries sit at positions n - q_len ..)
-  int kv_heads, causal;
-  float scale_log2;
+  int64_t nblk, ntiles;     // query blocks per (batch, KV head); 64-key tiles of n
+  int kv_heads, causal, neg;
+  float c;                  // |scale| * log2(e)
 };
 
 template <int DT> struct Mfma;
 template <> struct Mfma<TC_DTYPE_F16> {
-  static __device__ __forceinline__ float4v mma(const uint4& a, const uint4& b, float4v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+  static __device__ __forceinline__ float16v mma(const uint4& a, const uint4& b, const float16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
                                                   0, 0);
   }
 };
 template <> struct Mfma<TC_DTYPE_BF16> {
-  static __device__ __forceinline__ float4v mma(const uint4& a, const uint4& b, float4v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+  static __device__ __forceinline__ float16v mma(const uint4& a, const uint4& b, const float16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
   }
 };
+
+// Two fp32 values rounded to nearest even into one word of two 16-bit
+// elements (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32), the first in the low half.
+template <int DT> __device__ __forceinline__ uint32_t pack2(float x, float y);
+template <> __device__ __forceinline__ uint32_t pack2<TC_DTYPE_F16>(float x, float y) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <> __device__ __forceinline__ uint32_t pack2<TC_DTYPE_BF16>(float x, float y) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 v = {static_cast<__bf16>(x), static_cast<__bf16>(y)};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0,
@@ -86,6 +121,7 @@ struct Stage {
   uint4 v[4];
 };
 
+// Rows past n read as zeros (buffer range check); they are never visible.
 __device__ __forceinline__ void load_stage(Stage& s, const char* kslab, const char* vslab, int64_t row_k,
                                            int64_t row_v, int64_t key0, int64_t n) {
   const int t = threadIdx.x;
@@ -122,172 +158,247 @@ __device__ __forceinline__ void store_stage(const Stage& s, uint16_t* lk, uint16
   }
 }
 
-__device__ __forceinline__ float lanes4_max(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+// x combined with its value in lane l ^ 32 (v_permlane32_swap leaves both
+// halves' values in its two results).
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-
-__device__ __forceinline__ float lanes4_sum(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Key offset (within a 32-key half) of accumulator v of a lane in half `hi`.
+__device__ __forceinline__ int acc_key(int v, int hi) { return 8 * (v >> 2) + 4 * hi + (v & 3); }
+
 template <int DT, int G>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
-  using E = Elem<DT>;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_WAVES, TC_PREFILL_WAVES))) void prefill_kernel(
+    const PrefillArgs a) {
   constexpr int kTokens = kRows / G;   // query tokens per work-group
   __shared__ uint16_t s_k[2][kKTile];
   __shared__ uint16_t s_v[2][kVTile];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int quad = lane >> 4;          // 0..3
-  const int col = lane & 15;           // the lane's query row within the wave
-  // Causal blocks run longest first (the last query block sees the most keys).
-  const int64_t blk = a.causal ? static_cast<int64_t>(gridDim.x) - 1 - blockIdx.x : blockIdx.x;
-  const int64_t tok0 = blk * kTokens;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  const int hi = lane >> 5;            // which 16 keys of each 32-key half this lane holds
+  const int r32 = lane & 31;           // the lane's query row within the wave
 
-  // This lane's query row: (token, head of the group).
-  const int row = wave * 16 + col;
+  // Work item, KV heads fastest: consecutive work-groups go to different XCDs
+  // round-robin, so with 8 | kv_heads each XCD's L2 streams one head's K/V.
+  const int64_t wid = blockIdx.x;
+  const int h = static_cast<int>(wid % a.kv_heads);
+  const int64_t rest = wid / a.kv_heads;
+  int64_t blk = rest % a.nblk;
+  const int b = static_cast<int>(rest / a.nblk);
+  if (a.causal) blk = a.nblk - 1 - blk;  // longest rows first
+  const int64_t tok0 = blk * kTokens;
+
+  const int row = wave * 32 + r32;
   const int64_t tok = tok0 + row / G;
   const int hq = h * G + row % G;
   const bool row_ok = tok < a.q_len;
   const int64_t past = a.n - a.q_len;
-  const int64_t pos = past + tok;      // absolute position of the query token
 
-  // Q^T as the MFMA B operand: dims 32c + 8*quad .. +8 of this lane's row.
-  uint4 qb[4];
+  // Q^T as the MFMA B operand: dims 16c + 8*hi .. +8 of this lane's row.
+  uint4 qb[8];
   {
-    const uint16_t* qp = a.q + b * a.sq_b + hq * a.sq_h + (row_ok ? tok : 0) * a.sq_t + 8 * quad;
+    const uint16_t* qp = a.q + b * a.sq_b + hq * a.sq_h + (row_ok ? tok : 0) * a.sq_t + 8 * hi;
+    const uint32_t flip = a.neg ? 0x80008000u : 0u;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      qb[c] = row_ok ? *reinterpret_cast<const uint4*>(qp + 32 * c) : make_uint4(0u, 0u, 0u, 0u);
+    for (int c = 0; c < 8; ++c) {
+      uint4 x = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * c) : make_uint4(0u, 0u, 0u, 0u);
+      x.x ^= flip; x.y ^= flip; x.z ^= flip; x.w ^= flip;
+      qb[c] = x;
+    }
   }
 
   const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
   const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
   const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
-  const uint8_t* mrow = a.mask ? a.mask + b * a.sm_b + (row_ok ? tok : 0) * a.sm_q : nullptr;
+  const int64_t bm = a.sm_b ? b : 0;
+  const uint8_t* mrow = a.mask ? a.mask + bm * a.sm_b + (row_ok ? tok : 0) * a.sm_q : nullptr;
+  const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.ntiles : nullptr;
 
-  // Keys this work-group needs: all n, or up to its last query's position when causal.
+  // Tiles this work-group may need: all of n, or up to its last query's position when causal.
   const int64_t last_tok = min(tok0 + kTokens, a.q_len) - 1;
   const int64_t key_end = a.causal ? min(a.n, past + last_tok + 1) : a.n;
-  const int64_t ntiles = (key_end + kKeys - 1) / kKeys;
+  const int64_t nt = (key_end + kKeys - 1) / kKeys;
+  auto tile_class = [&](int64_t t) -> int {
+    if (tcls) return tcls[t];
+    if (a.mask) return TILE_MIXED;
+    const int64_t key0 = t * kKeys;
+    if (key0 + kKeys > a.n) return TILE_MIXED;
+    if (a.causal && key0 + kKeys - 1 > past + tok0) return TILE_MIXED;
+    return TILE_FULL;
+  };
+  auto next_active = [&](int64_t t) -> int64_t {
+    while (t < nt && tile_class(t) == TILE_SKIP) ++t;
+    return t;
+  };
 
   float m = neg_inf(), l = 0.f;
-  float4v o[8];
+  float16v o[4];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[dt][v] = 0.f;
 
   Stage st;
-  if (ntiles > 0) {
-    load_stage(st, kslab, vslab, row_k, row_v, 0, a.n);
+  int64_t t = next_active(0);
+  if (t < nt) {
+    load_stage(st, kslab, vslab, row_k, row_v, t * kKeys, a.n);
     store_stage(st, s_k[0], s_v[0]);
   }
   __syncthreads();
 
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const int buf = static_cast<int>(t & 1);
-    const bool more = t + 1 < ntiles;
-    if (more) load_stage(st, kslab, vslab, row_k, row_v, (t + 1) * kKeys, a.n);
+  int buf = 0;
+  while (t < nt) {
+    const int64_t tn = next_active(t + 1);
+    const bool more = tn < nt;
+    if (more) load_stage(st, kslab, vslab, row_k, row_v, tn * kKeys, a.n);
+    const int cls = tile_class(t);
 
-    // S^T tile: 4 groups of 16 keys; lane holds keys 16*kt + 4*quad + r.
     const uint16_t* lk = s_k[buf];
-    float4v s[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      float4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint4 ka = *reinterpret_cast<const uint4*>(lk + (16 * kt + col) * kKStride + 32 * c + 8 * quad);
-        acc = Mfma<DT>::mma(ka, qb[c], acc);
-      }
-      s[kt] = acc;
-    }
-
-    // Scale, mask, running max of this row (4 lanes hold its 64 keys).
-    const int64_t key0 = t * kKeys;
-    float tmax = neg_inf();
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t key = key0 + 16 * kt + 4 * quad + r;
-        bool ok = row_ok && key < a.n && (!a.causal || key <= pos);
-        if (ok && mrow) ok = mrow[key * a.sm_k] != 0;
-        const float x = ok ? s[kt][r] * a.scale_log2 : neg_inf();
-        s[kt][r] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = lanes4_max(tmax);
-    const float mn = fmaxf(m, tmax);
-    const float ms = (mn == neg_inf()) ? 0.f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(m - ms);
-    m = mn;
-
-    // P^T as the B operand of two 32-key MFMA chunks: keys {4q..4q+3} of
-    // group 2*kc and of group 2*kc+1, in that order (V^T is read to match).
-    uint4 pb[2];
-    float psum = 0.f;
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-      uint32_t w[4];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const float4v& x = s[2 * kc + half];
-        const float p0 = __builtin_amdgcn_exp2f(x[0] - ms), p1 = __builtin_amdgcn_exp2f(x[1] - ms);
-        const float p2 = __builtin_amdgcn_exp2f(x[2] - ms), p3 = __builtin_amdgcn_exp2f(x[3] - ms);
-        psum += (p0 + p1) + (p2 + p3);
-        w[2 * half] = E::bits(p0) | (E::bits(p1) << 16);
-        w[2 * half + 1] = E::bits(p2) | (E::bits(p3) << 16);
-      }
-      pb[kc] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-    l = l * alpha + psum;
-
     const uint16_t* lv = s_v[buf];
+    const int64_t key0 = t * kKeys;
+    // Visible-key limit of this lane's row on a MIXED tile (keys of the tile below it).
+    int lim = kKeys;
+    const uint8_t* mt = nullptr;
+    if (cls == TILE_MIXED) {
+      int64_t lim64 = a.n - key0;
+      if (a.causal) lim64 = min(lim64, past + tok + 1 - key0);
+      lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
+      mt = mrow ? mrow + key0 : nullptr;
+    }
+
+    // The tile in two 32-key halves, each a full online-softmax step.
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      float4v acc = o[dt] * alpha;
+    for (int kt = 0; kt < 2; ++kt) {
+      float16v s;
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const uint16_t* vp = lv + (16 * dt + col) * kVStride + 32 * kc + 4 * quad;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vp + 16);
-        acc = Mfma<DT>::mma(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[kc], acc);
+      for (int v = 0; v < 16; ++v) s[v] = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint4 ka = *reinterpret_cast<const uint4*>(lk + (32 * kt + r32) * kKStride + 16 * c + 8 * hi);
+        s = Mfma<DT>::mma(ka, qb[c], s);
       }
-      o[dt] = acc;
+
+      // Visible keys of this lane (bit v), all of them on a FULL tile.
+      uint32_t vis = 0xffffu;
+      if (cls == TILE_MIXED) {
+        vis = 0;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = 32 * kt + acc_key(v, hi);
+          bool ok = key < lim;
+          if (mt && ok) ok = mt[key] != 0;
+          vis |= ok ? (1u << v) : 0u;
+        }
+      }
+
+      // Row maximum of the raw scores (c >= 0, so max(s * c) = c * max(s)).
+      float mx = neg_inf();
+      if (cls == TILE_MIXED) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, (vis >> v) & 1u ? s[v] : neg_inf());
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
+      }
+      mx = pair_max(mx);
+      const float mn = fmaxf(m, mx == neg_inf() ? neg_inf() : mx * a.c);
+      const float ms = (mn == neg_inf()) ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);
+      m = mn;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[dt][v] *= alpha;
+      }
+
+      // P^T operand of chunk c2: accumulators 8*c2 .. 8*c2+7 are keys
+      // 16*c2 + {4hi..4hi+3, 8+4hi..8+4hi+3} of the half, the order in which
+      // V^T is read.
+      float psum = 0.f;
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int v0 = 8 * c2 + 2 * j;
+          float p0 = __builtin_amdgcn_exp2f(fmaf(s[v0], a.c, -ms));
+          float p1 = __builtin_amdgcn_exp2f(fmaf(s[v0 + 1], a.c, -ms));
+          if (cls == TILE_MIXED) {
+            p0 = (vis >> v0) & 1u ? p0 : 0.f;
+            p1 = (vis >> (v0 + 1)) & 1u ? p1 : 0.f;
+          }
+          psum += p0 + p1;
+          w[j] = pack2<DT>(p0, p1);
+        }
+        const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const uint16_t* vp = lv + (32 * dt + r32) * kVStride + 32 * kt + 16 * c2 + 4 * hi;
+          const uint2 lo = *reinterpret_cast<const uint2*>(vp);
+          const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
+          o[dt] = Mfma<DT>::mma(make_uint4(lo.x, lo.y, up.x, up.y), pb, o[dt]);
+        }
+      }
+      l = l * alpha + psum;
     }
 
     if (more) store_stage(st, s_k[buf ^ 1], s_v[buf ^ 1]);
     __syncthreads();
+    buf ^= 1;
+    t = tn;
   }
 
-  // Normalize and write this lane's 32 outputs (dims 16*dt + 4*quad + r).
-  const float lt = lanes4_sum(l);
+  // Normalize and write this lane's 64 outputs: dims 32*dt + 8*j + 4*hi + 0..3.
+  const float lt = pair_sum(l);
   if (row_ok) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    uint16_t* op = a.out + b * a.so_b + tok * a.so_t + hq * a.so_h + 4 * quad;
+    uint16_t* op = a.out + b * a.so_b + tok * a.so_t + hq * a.so_h + 4 * hi;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint32_t w0 = E::bits(o[dt][0] * inv) | (E::bits(o[dt][1] * inv) << 16);
-      const uint32_t w1 = E::bits(o[dt][2] * inv) | (E::bits(o[dt][3] * inv) << 16);
-      *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(w0, w1);
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w0 = pack2<DT>(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv);
+        const uint32_t w1 = pack2<DT>(o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 32 * dt + 8 * j) = make_uint2(w0, w1);
+      }
+  }
+}
+
+// One wave per (64-key tile, query block, mask batch): lane = key in the tile.
+__global__ __launch_bounds__(64) void mask_tiles_kernel(const uint8_t* mask, int64_t sm_b, int64_t sm_q,
+                                                       int64_t sm_k, int64_t q_len, int64_t n, int tokens,
+                                                       int64_t nblk, int64_t ntiles, uint8_t* tiles) {
+  const int lane = threadIdx.x;
+  const int64_t t = blockIdx.x, blk = blockIdx.y, bm = blockIdx.z;
+  const int64_t key = t * kKeys + lane;
+  const int64_t tok0 = blk * tokens;
+  const int64_t tok_end = min(tok0 + tokens, q_len);
+  bool any = false, all = key < n;
+  if (key < n) {
+    const uint8_t* p = mask + bm * sm_b + key * sm_k;
+    for (int64_t tok = tok0; tok < tok_end; ++tok) {
+      const bool x = p[tok * sm_q] != 0;
+      any |= x;
+      all &= x;
     }
   }
+  const uint64_t any_w = __builtin_amdgcn_ballot_w64(any);
+  const uint64_t all_w = __builtin_amdgcn_ballot_w64(all);
+  if (lane == 0)
+    tiles[(bm * nblk + blk) * ntiles + t] =
+        static_cast<uint8_t>(any_w == 0 ? TILE_SKIP : (all_w == ~uint64_t(0) ? TILE_FULL : TILE_MIXED));
 }
 
 template <int DT>
 hipError_t launch_dt(const PrefillArgs& a, int group, int batch, hipStream_t stream) {
-  const int tokens = kRows / group;
-  const dim3 grid(static_cast<unsigned>((a.q_len + tokens - 1) / tokens), static_cast<unsigned>(a.kv_heads),
-                  static_cast<unsigned>(batch));
+  const dim3 grid(static_cast<unsigned>(a.nblk * a.kv_heads * batch));
   switch (group) {
     case 1: hipLaunchKernelGGL((prefill_kernel<DT, 1>), grid, dim3(256), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((prefill_kernel<DT, 2>), grid, dim3(256), 0, stream, a); break;
@@ -306,24 +417,86 @@ int check3(const char* what, const int64_t* st) {
   return TC_OK;
 }
 
+int check_group(int q_heads, int kv_heads, int* group) {
+  if (kv_heads < 1 || kv_heads > 65535 || q_heads < 1)
+    return fail(TC_ERR_INVALID_ARGUMENT, "q_heads %d, kv_heads %d", q_heads, kv_heads);
+  if (q_heads % kv_heads)
+    return fail(TC_ERR_INVALID_ARGUMENT, "q_heads %d not a multiple of kv_heads %d", q_heads, kv_heads);
+  *group = q_heads / kv_heads;
+  if (*group != 1 && *group != 2 && *group != 4 && *group != 8)
+    return fail(TC_ERR_UNSUPPORTED, "group %d unsupported (1, 2, 4 or 8)", *group);
+  return TC_OK;
+}
+
+int check_mask_strides(const int64_t* st) {
+  if (!st) return fail(TC_ERR_INVALID_ARGUMENT, "mask strides are null");
+  if (st[0] < 0 || st[1] < 0 || st[2] < 0) return fail(TC_ERR_INVALID_ARGUMENT, "mask strides must be non-negative");
+  if (st[2] != 1) return fail(TC_ERR_UNSUPPORTED, "mask keys must be contiguous (key stride %lld)", (long long)st[2]);
+  return TC_OK;
+}
+
+// Tile map geometry: query blocks of 128/g tokens, 64-key tiles.
+void tile_geometry(int64_t q_len, int64_t n, int group, int64_t* nblk, int64_t* ntiles) {
+  const int64_t tokens = kRows / group;
+  *nblk = (q_len + tokens - 1) / tokens;
+  *ntiles = (n + kKeys - 1) / kKeys;
+}
+
 }  // namespace
 }  // namespace tc
 
 using namespace tc;
 
+extern "C" size_t tc_prefill_tiles_bytes(int64_t q_len, int64_t n_tokens, int mask_batch, int q_heads,
+                                         int kv_heads) {
+  int group = 0;
+  if (q_len < 0 || n_tokens < q_len || mask_batch < 1 || check_group(q_heads, kv_heads, &group) != TC_OK) return 0;
+  int64_t nblk, ntiles;
+  tile_geometry(q_len, n_tokens, group, &nblk, &ntiles);
+  return static_cast<size_t>(mask_batch * nblk * ntiles);
+}
+
+extern "C" int tc_prefill_mask_tiles(const uint8_t* mask_dev, const int64_t mask_strides[3], int mask_batch,
+                                     int64_t q_len, int64_t n_tokens, int q_heads, int kv_heads, uint8_t* tiles_dev,
+                                     size_t tiles_bytes, void* stream) {
+  clear_error();
+  int group = 0, rc;
+  if ((rc = check_group(q_heads, kv_heads, &group)) != TC_OK) return rc;
+  if (mask_batch < 1 || mask_batch > 65535) return fail(TC_ERR_INVALID_ARGUMENT, "mask_batch %d", mask_batch);
+  if (q_len < 0 || n_tokens < q_len)
+    return fail(TC_ERR_INVALID_ARGUMENT, "q_len %lld must be in [0, n_tokens %lld]", (long long)q_len,
+                (long long)n_tokens);
+  if ((rc = check_mask_strides(mask_strides)) != TC_OK) return rc;
+  if (mask_batch > 1 && mask_strides[0] == 0)
+    return fail(TC_ERR_INVALID_ARGUMENT, "mask_batch %d with a broadcast (stride 0) mask batch", mask_batch);
+  int64_t nblk, ntiles;
+  tile_geometry(q_len, n_tokens, group, &nblk, &ntiles);
+  const size_t need = static_cast<size_t>(mask_batch * nblk * ntiles);
+  if (need == 0) return TC_OK;
+  if (!mask_dev || !tiles_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null mask or tile map pointer");
+  if (tiles_bytes < need)
+    return fail(TC_ERR_WORKSPACE, "tile map holds %zu bytes, needs %zu", tiles_bytes, need);
+  if (ntiles > 0x7fffffff || nblk > 65535)
+    return fail(TC_ERR_UNSUPPORTED, "mask of %lld x %lld exceeds the tile grid", (long long)q_len,
+                (long long)n_tokens);
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(nblk), static_cast<unsigned>(mask_batch));
+  hipLaunchKernelGGL(mask_tiles_kernel, grid, dim3(64), 0, static_cast<hipStream_t>(stream), mask_dev,
+                     mask_strides[0], mask_strides[1], mask_strides[2], q_len, n_tokens, kRows / group, nblk, ntiles,
+                     tiles_dev);
+  return hip_status(hipGetLastError(), "mask tile launch");
+}
+
 extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3], const void* k_dev,
                                     const int64_t k_strides[3], const void* v_dev, const int64_t v_strides[3],
-                                    const uint8_t* mask_dev, const int64_t mask_strides[3], int causal,
+                                    const uint8_t* mask_dev, const int64_t mask_strides[3],
+                                    const uint8_t* mask_tiles_dev, size_t mask_tiles_bytes, int causal,
                                     int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
                                     int head_dim, int dtype, float scale, void* out_dev,
                                     const int64_t out_strides[3], void* stream) {
   clear_error();
-  if (batch < 1 || batch > 65535 || kv_heads < 1 || kv_heads > 65535 || q_heads < 1)
-    return fail(TC_ERR_INVALID_ARGUMENT, "batch %d, q_heads %d, kv_heads %d", batch, q_heads, kv_heads);
-  if (q_heads % kv_heads) return fail(TC_ERR_INVALID_ARGUMENT, "q_heads %d not a multiple of kv_heads %d", q_heads, kv_heads);
-  const int group = q_heads / kv_heads;
-  if (group != 1 && group != 2 && group != 4 && group != 8)
-    return fail(TC_ERR_UNSUPPORTED, "group %d unsupported (1, 2, 4 or 8)", group);
+  int group = 0, rc;
+  if (batch < 1 || batch > 65535) return fail(TC_ERR_INVALID_ARGUMENT, "batch %d", batch);
+  if ((rc = check_group(q_heads, kv_heads, &group)) != TC_OK) return rc;
   if (head_dim != kHeadDim) return fail(TC_ERR_UNSUPPORTED, "head_dim %d unsupported (kernels are built for 128)", head_dim);
   if (dtype != TC_DTYPE_F16 && dtype != TC_DTYPE_BF16) return fail(TC_ERR_UNSUPPORTED, "dtype %d unsupported", dtype);
   if (q_len < 0 || n_tokens < q_len)
@@ -333,7 +506,6 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
   if (!q_dev || !k_dev || !v_dev || !out_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null tensor pointer");
   if (!aligned16(q_dev) || !aligned16(k_dev) || !aligned16(v_dev) || !aligned16(out_dev))
     return fail(TC_ERR_ALIGNMENT, "q/k/v/out base pointers must be 16-byte aligned");
-  int rc;
   if ((rc = check3("q", q_strides)) != TC_OK) return rc;
   if ((rc = check3("k", k_strides)) != TC_OK) return rc;
   if ((rc = check3("v", v_strides)) != TC_OK) return rc;
@@ -343,30 +515,43 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
   if (k_strides[2] < head_dim || v_strides[2] < head_dim || k_strides[2] >= kMaxTokenStride ||
       v_strides[2] >= kMaxTokenStride)
     return fail(TC_ERR_INVALID_ARGUMENT, "k/v token strides outside [%d, 2^24)", head_dim);
-  if (mask_dev && !mask_strides) return fail(TC_ERR_INVALID_ARGUMENT, "mask strides are null");
-  if (mask_dev && causal) return fail(TC_ERR_INVALID_ARGUMENT, "pass either a mask or causal, not both");
-  if (mask_dev && (mask_strides[0] < 0 || mask_strides[1] < 0 || mask_strides[2] < 0))
-    return fail(TC_ERR_INVALID_ARGUMENT, "mask strides must be non-negative");
   if (!std::isfinite(scale)) return fail(TC_ERR_INVALID_ARGUMENT, "scale is not finite");
+  int64_t nblk, ntiles;
+  tile_geometry(q_len, n_tokens, group, &nblk, &ntiles);
+  if (nblk * kv_heads * batch > 0x7fffffff) return fail(TC_ERR_UNSUPPORTED, "grid too large");
+  if (mask_dev) {
+    if (causal) return fail(TC_ERR_INVALID_ARGUMENT, "pass either a mask or causal, not both");
+    if ((rc = check_mask_strides(mask_strides)) != TC_OK) return rc;
+    if (mask_tiles_dev) {
+      const size_t need = static_cast<size_t>((mask_strides[0] ? batch : 1) * nblk * ntiles);
+      if (mask_tiles_bytes < need)
+        return fail(TC_ERR_WORKSPACE, "tile map holds %zu bytes, this call reads %zu", mask_tiles_bytes, need);
+    }
+  } else if (mask_tiles_dev) {
+    return fail(TC_ERR_INVALID_ARGUMENT, "a tile map without its mask");
+  }
 
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q_dev);
   a.k = static_cast<const uint16_t*>(k_dev);
   a.v = static_cast<const uint16_t*>(v_dev);
   a.mask = mask_dev;
+  a.tiles = mask_dev ? mask_tiles_dev : nullptr;
   a.out = static_cast<uint16_t*>(out_dev);
   a.sq_b = q_strides[0]; a.sq_h = q_strides[1]; a.sq_t = q_strides[2];
   a.sk_b = k_strides[0]; a.sk_h = k_strides[1]; a.sk_t = k_strides[2];
   a.sv_b = v_strides[0]; a.sv_h = v_strides[1]; a.sv_t = v_strides[2];
   a.sm_b = mask_dev ? mask_strides[0] : 0;
   a.sm_q = mask_dev ? mask_strides[1] : 0;
-  a.sm_k = mask_dev ? mask_strides[2] : 0;
   a.so_b = out_strides[0]; a.so_t = out_strides[1]; a.so_h = out_strides[2];
   a.q_len = q_len;
   a.n = n_tokens;
+  a.nblk = nblk;
+  a.ntiles = ntiles;
   a.kv_heads = kv_heads;
   a.causal = causal ? 1 : 0;
-  a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  a.neg = scale < 0.f ? 1 : 0;
+  a.c = static_cast<float>(std::fabs(static_cast<double>(scale)) * 1.4426950408889634);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == TC_DTYPE_F16 ? launch_dt<TC_DTYPE_F16>(a, group, batch, s)
                                              : launch_dt<TC_DTYPE_BF16>(a, group, batch, s);

@@ -9,6 +9,8 @@ once for all of them and runs QKᵀ and PV on the matrix cores with an fp32
 online softmax. This module checks tensors and passes pointers, strides and
 the current stream.
 """
+import weakref
+
 import torch
 
 from . import _lib
@@ -40,6 +42,13 @@ def _strides(t, dims, token_dim=None):
     return _lib.i64x3(*st)
 
 
+def _mask_strides(m):
+    """Strides of a [mb, q, n] mask view; keys are contiguous (stride 1)."""
+    st = _strides(m, (0, 1, 2))
+    st[2] = 1
+    return st
+
+
 def prefill_attention(query, key, value, attention_mask=None, scale=None, is_causal=False, out=None):
     """SDPA(query, repeat_kv(key, g), repeat_kv(value, g), attention_mask, scale,
     is_causal).transpose(1, 2) without expanding K/V.
@@ -69,20 +78,53 @@ def prefill_attention(query, key, value, attention_mask=None, scale=None, is_cau
         out = torch.empty((b, q, hq, d), dtype=query.dtype, device=query.device)
     elif out.shape != (b, q, hq, d) or out.dtype != query.dtype or out.device != query.device or out.stride(3) != 1:
         raise ValueError("prefill_attention: out must be [b, q, hq, d] in query's dtype and device")
-    mask_ptr, mask_strides = None, None
+    mask_ptr, mask_strides, tiles = None, None, None
     if attention_mask is not None:
         m = attention_mask
         if m.dtype != torch.bool or m.dim() != 4 or m.shape[1] != 1 or m.shape[0] not in (1, b) \
                 or tuple(m.shape[2:]) != (q, n) or m.device != query.device:
             raise ValueError(f"prefill_attention: attention_mask must be bool [b|1, 1, {q}, {n}] on the device")
+        if m.stride(3) != 1 and n > 1:  # the kernels read mask rows as contiguous bytes
+            m = m.contiguous()
+        tiles = mask_tiles(m, hq, hkv)
         m = m[:, 0]
-        mask_ptr, mask_strides = m.data_ptr(), _strides(m, (0, 1, 2))
+        mask_ptr, mask_strides = m.data_ptr(), _mask_strides(m)
     scale = scale if scale is not None else d ** -0.5
     lib = _lib.load()
     rc = lib.tc_prefill_attention(
         query.data_ptr(), _strides(query, (0, 1, 2)), key.data_ptr(), _strides(key, (0, 1, 2), 2),
-        value.data_ptr(), _strides(value, (0, 1, 2), 2), mask_ptr, mask_strides, int(bool(is_causal)),
+        value.data_ptr(), _strides(value, (0, 1, 2), 2), mask_ptr, mask_strides,
+        None if tiles is None else tiles.data_ptr(), 0 if tiles is None else tiles.numel(), int(bool(is_causal)),
         q, n, b, hq, hkv, d, _lib.dtype_code(query.dtype), float(scale),
         out.data_ptr(), _strides(out, (0, 1, 2)), _lib.stream_of(query.device))
     _lib.check(rc, "tc_prefill_attention")
     return out
+
+
+# The tile map of the last mask seen. transformers builds one mask per forward
+# pass and hands the same tensor to every layer, so the map is built once per
+# pass; it is rebuilt when the mask object, its version or the geometry change.
+_tile_cache = None
+
+
+def mask_tiles(mask, q_heads, kv_heads):
+    """uint8 tile map of a bool mask [b|1, 1, q, n] (``tc_prefill_mask_tiles``), cached per mask."""
+    global _tile_cache
+    key = (mask._version, tuple(mask.shape), tuple(mask.stride()), mask.data_ptr(), q_heads, kv_heads)
+    c = _tile_cache
+    if c is not None and c[0]() is mask and c[1] == key:
+        return c[2]
+    m = mask[:, 0]
+    mb = m.shape[0] if m.shape[0] > 1 and m.stride(0) != 0 else 1
+    q, n = m.shape[1], m.shape[2]
+    lib = _lib.load()
+    nbytes = lib.tc_prefill_tiles_bytes(q, n, mb, q_heads, kv_heads)
+    tiles = torch.empty(max(1, nbytes), dtype=torch.uint8, device=mask.device)
+    st = _mask_strides(m)
+    if mb == 1:
+        st[0] = 0
+    rc = lib.tc_prefill_mask_tiles(m.data_ptr(), st, mb, q, n, q_heads, kv_heads, tiles.data_ptr(), tiles.numel(),
+                                   _lib.stream_of(mask.device))
+    _lib.check(rc, "tc_prefill_mask_tiles")
+    _tile_cache = (weakref.ref(mask), key, tiles)
+    return tiles
