@@ -208,7 +208,9 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
  * A query row with no visible key gets zeros. q [b, hq, q_len, d] and k/v
  * [b, hkv, n_tokens, d] with element strides {batch, head, token} and a
  * contiguous last dim; out [b, q_len, hq, d] with strides {batch, token,
- * head}. head_dim must be 128, g one of 1, 2, 4, 8. */
+ * head}. head_dim must be 128, g one of 1, 2, 4, 8. num_splits <= 0 picks
+ * the key split count (tc_prefill_num_splits); the workspace must hold
+ * tc_prefill_workspace_bytes for the count used (none for one split). */
 int tc_prefill_attention(const void* q, const int64_t q_strides[3],
                          const void* k, const int64_t k_strides[3],
                          const void* v, const int64_t v_strides[3],
@@ -216,7 +218,19 @@ int tc_prefill_attention(const void* q, const int64_t q_strides[3],
                          const uint8_t* mask_tiles, size_t mask_tiles_bytes, int causal,
                          int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
                          int head_dim, int dtype, float scale,
+                         int num_splits, void* workspace, size_t workspace_bytes,
                          void* out, const int64_t out_strides[3], void* stream);
+
+/* Key splits tc_prefill_attention uses with num_splits <= 0 (a negative value
+ * is -TC_ERR_*): 1 when the query blocks (128 rows of one KV head each) give
+ * every compute unit two work-groups, else enough splits of the keys to do
+ * so, merged by a log-sum-exp combine pass. A short chunk on top of a long
+ * cache (the engine's prefill after a splice) is the case this covers. */
+int tc_prefill_num_splits(int batch, int64_t q_len, int64_t n_tokens, int q_heads, int kv_heads);
+
+/* Workspace bytes of a call with num_splits splits (0 for one split): fp32
+ * partial outputs [b, splits, q_len, hq, d] then log-sum-exps [b, splits, q_len, hq]. */
+size_t tc_prefill_workspace_bytes(int batch, int64_t q_len, int q_heads, int num_splits);
 
 /* Bytes of the tile map of a mask with mask_batch distinct batch entries
  * (1 for a broadcast mask); 0 for invalid sizes. */

@@ -34,10 +34,10 @@ def torch_route(q, k, v, mask, causal, scale=SCALE):
     return out.transpose(1, 2)
 
 
-def check(q, k, v, mask=None, causal=False, scale=SCALE, label=""):
+def check(q, k, v, mask=None, causal=False, scale=SCALE, label="", splits=None):
     print(f"case: {label} q={tuple(q.shape)} k={tuple(k.shape)} dtype={q.dtype} causal={causal} "
-          f"mask={None if mask is None else tuple(mask.shape)}", flush=True)
-    out = prefill.prefill_attention(q, k, v, mask, scale, causal)
+          f"mask={None if mask is None else tuple(mask.shape)} splits={splits}", flush=True)
+    out = prefill.prefill_attention(q, k, v, mask, scale, causal, splits=splits)
     torch.cuda.synchronize()
     assert out.shape == (q.shape[0], q.shape[2], q.shape[1], q.shape[3]) and out.is_contiguous()
     want = ref64(q, k, v, mask, causal, scale)
@@ -83,6 +83,31 @@ def test_random_masks_and_batches(gpu, batch_mask):
     m = torch.rand((batch_mask, 1, L, n), generator=g) < 0.3
     m[..., 7] = True
     check(q, k, v, mask=m.to(gpu), label=f"random mask batch {batch_mask}")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16])
+def test_key_splits(gpu, splits):
+    """Splitting the keys across work-groups (LSE-merged) gives the same attention,
+    for causal, masked-chunk and unmasked calls; more splits than tiles are clamped."""
+    q, k, v = workloads.prefill_inputs(20 + splits, q_len=200, n=200, device=gpu)
+    check(q, k, v, causal=True, splits=splits, label="split causal")
+    q, k, v = workloads.prefill_inputs(30 + splits, q_len=70, n=900, device=gpu)
+    check(q, k, v, mask=workloads.causal_mask(70, 900).to(gpu), splits=splits, label="split chunk")
+    check(q, k, v, splits=splits, label="split full")
+    g = torch.Generator().manual_seed(splits)
+    m = torch.rand((1, 1, 70, 900), generator=g) < 0.05
+    m[..., :3, :] = False  # rows with no visible key in any split
+    out = check(q, k, v, mask=m.to(gpu), splits=splits, label="split sparse mask")
+    assert torch.all(out[0, :3] == 0)
+
+
+def test_short_chunk_on_long_cache_uses_splits(gpu):
+    """A few hundred new tokens on top of a 10k cache: too few query blocks to fill
+    the GPU, so the keys are split."""
+    assert prefill.num_splits(1, 300, 10000, 32, 8) > 1
+    assert prefill.num_splits(1, 2048, 9764, 32, 8) == 1
+    q, k, v = workloads.prefill_inputs(40, q_len=300, n=10000, device=gpu)
+    check(q, k, v, mask=workloads.causal_mask(300, 10000).to(gpu), label="short chunk")
 
 
 def test_rows_without_visible_keys_are_zero(gpu):
@@ -155,6 +180,5 @@ def test_rejects(gpu):
         lib = _lib.load()
         rc = lib.tc_prefill_attention(q.data_ptr(), _lib.i64x3(0, 0, 0), k.data_ptr(), _lib.i64x3(0, 0, 128),
                                       v.data_ptr(), _lib.i64x3(0, 0, 128), None, None, None, 0, 1, 9, 8, 1, 32, 8,
-                                      128, 0,
-                                      SCALE, q.data_ptr(), _lib.i64x3(0, 0, 0), None)
+                                      128, 0, SCALE, 1, None, 0, q.data_ptr(), _lib.i64x3(0, 0, 0), None)
         _lib.check(rc, "tc_prefill_attention")

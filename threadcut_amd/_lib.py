@@ -54,7 +54,9 @@ SIGNATURES = {
     "tc_splice_copy": (_I, [_PP, _PP, _I64P, _I64, _PP, _PP, _I64P, _I, _I, _I, _I, _I, _I64, _I64, _I64,
                             _FP, _P]),
     "tc_prefill_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _S, _I, _I64, _I64, _I, _I,
-                                  _I, _I, _I, _F, _P, _I64P, _P]),
+                                  _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
+    "tc_prefill_num_splits": (_I, [_I, _I64, _I64, _I, _I]),
+    "tc_prefill_workspace_bytes": (_S, [_I, _I64, _I, _I]),
     "tc_prefill_tiles_bytes": (_S, [_I64, _I64, _I, _I, _I]),
     "tc_prefill_mask_tiles": (_I, [_P, _I64P, _I, _I64, _I64, _I, _I, _P, _S, _P]),
     "tc_match_split": (_I, [_I64P, _I64, _I64P, _I64, _I64, _I, _I64P]),

@@ -71,7 +71,10 @@ struct PrefillArgs {
   int64_t so_b, so_t, so_h;
   int64_t q_len, n;         // query tokens, keys (the queries sit at positions n - q_len ..)
   int64_t nblk, ntiles;     // query blocks per (batch, KV head); 64-key tiles of n
-  int kv_heads, causal, neg;
+  int64_t split_tiles;      // tiles per key split
+  float* o_part;            // splits > 1: [b, splits, L, hq, d] fp32, normalized per split
+  float* lse_part;          // splits > 1: [b, splits, L, hq] log2-sum-exp of the split (-inf if empty)
+  int kv_heads, causal, neg, splits;
   float c;                  // |scale| * log2(e)
 };
 
@@ -184,11 +187,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const int hi = lane >> 5;            // which 16 keys of each 32-key half this lane holds
   const int r32 = lane & 31;           // the lane's query row within the wave
 
-  // Work item, KV heads fastest: consecutive work-groups go to different XCDs
-  // round-robin, so with 8 | kv_heads each XCD's L2 streams one head's K/V.
+  // Work item (KV head fastest, then key split, query block, batch):
+  // consecutive work-groups go to different XCDs round-robin, so with
+  // 8 | kv_heads each XCD's L2 streams one head's K/V.
   const int64_t wid = blockIdx.x;
   const int h = static_cast<int>(wid % a.kv_heads);
-  const int64_t rest = wid / a.kv_heads;
+  int64_t rest = wid / a.kv_heads;
+  const int split = static_cast<int>(rest % a.splits);
+  rest /= a.splits;
   int64_t blk = rest % a.nblk;
   const int b = static_cast<int>(rest / a.nblk);
   if (a.causal) blk = a.nblk - 1 - blk;  // longest rows first
@@ -220,10 +226,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const uint8_t* mrow = a.mask ? a.mask + bm * a.sm_b + (row_ok ? tok : 0) * a.sm_q : nullptr;
   const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.ntiles : nullptr;
 
-  // Tiles this work-group may need: all of n, or up to its last query's position when causal.
+  // Tiles this work-group may need: its split's share of all n keys, cut at
+  // its last query's position when causal.
   const int64_t last_tok = min(tok0 + kTokens, a.q_len) - 1;
   const int64_t key_end = a.causal ? min(a.n, past + last_tok + 1) : a.n;
-  const int64_t nt = (key_end + kKeys - 1) / kKeys;
+  const int64_t t_begin = split * a.split_tiles;
+  const int64_t nt = min((key_end + kKeys - 1) / kKeys, t_begin + a.split_tiles);
   auto tile_class = [&](int64_t t) -> int {
     if (tcls) return tcls[t];
     if (a.mask) return TILE_MIXED;
@@ -245,7 +253,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     for (int v = 0; v < 16; ++v) o[dt][v] = 0.f;
 
   Stage st;
-  int64_t t = next_active(0);
+  int64_t t = next_active(t_begin);
   if (t < nt) {
     load_stage(st, kslab, vslab, row_k, row_v, t * kKeys, a.n);
     store_stage(st, s_k[0], s_v[0]);
@@ -357,8 +365,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
   // Normalize and write this lane's 64 outputs: dims 32*dt + 8*j + 4*hi + 0..3.
   const float lt = pair_sum(l);
-  if (row_ok) {
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (!row_ok) return;
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (a.splits == 1) {
     uint16_t* op = a.out + b * a.so_b + tok * a.so_t + hq * a.so_h + 4 * hi;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -368,7 +377,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
         const uint32_t w1 = pack2<DT>(o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
         *reinterpret_cast<uint2*>(op + 32 * dt + 8 * j) = make_uint2(w0, w1);
       }
+    return;
   }
+  // Partial of this key split, merged by prefill_combine_kernel.
+  const int64_t prow = ((static_cast<int64_t>(b) * a.splits + split) * a.q_len + tok) * (a.kv_heads * G) + hq;
+  float* op = a.o_part + prow * kHeadDim + 4 * hi;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<float4*>(op + 32 * dt + 8 * j) =
+          make_float4(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
+  if (hi == 0) a.lse_part[prow] = lt > 0.f ? m + __log2f(lt) : neg_inf();
+}
+
+// out[b, tok, hq, :] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the key
+// splits (M = max_s lse_s); zeros when no split saw a key. 8 rows per
+// 256-thread work-group, 4 dims per thread.
+template <int DT>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const float* o_part, const float* lse_part,
+                                                              int splits, int64_t q_len, int hq_total,
+                                                              uint16_t* out, int64_t so_b, int64_t so_t,
+                                                              int64_t so_h) {
+  const int64_t rows = q_len * hq_total;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  const int b = blockIdx.y;
+  if (row >= rows) return;
+  const int d0 = 4 * (threadIdx.x & 31);
+  const float* lp = lse_part + static_cast<int64_t>(b) * splits * rows + row;
+  float mx = neg_inf();
+  for (int s = 0; s < splits; ++s) mx = fmaxf(mx, lp[s * rows]);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float wsum = 0.f;
+  if (mx != neg_inf()) {
+    const float* opp = o_part + (static_cast<int64_t>(b) * splits * rows + row) * kHeadDim + d0;
+    for (int s = 0; s < splits; ++s) {
+      const float w = __builtin_amdgcn_exp2f(lp[s * rows] - mx);
+      const float4 x = *reinterpret_cast<const float4*>(opp + s * rows * kHeadDim);
+      acc.x += w * x.x; acc.y += w * x.y; acc.z += w * x.z; acc.w += w * x.w;
+      wsum += w;
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  const int64_t tok = row / hq_total;
+  const int hq = static_cast<int>(row % hq_total);
+  uint16_t* op = out + b * so_b + tok * so_t + hq * so_h + d0;
+  *reinterpret_cast<uint2*>(op) = make_uint2(pack2<DT>(acc.x * inv, acc.y * inv), pack2<DT>(acc.z * inv, acc.w * inv));
 }
 
 // One wave per (64-key tile, query block, mask batch): lane = key in the tile.
@@ -398,13 +452,19 @@ __global__ __launch_bounds__(64) void mask_tiles_kernel(const uint8_t* mask, int
 
 template <int DT>
 hipError_t launch_dt(const PrefillArgs& a, int group, int batch, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(a.nblk * a.kv_heads * batch));
+  const dim3 grid(static_cast<unsigned>(a.nblk * a.kv_heads * batch * a.splits));
   switch (group) {
     case 1: hipLaunchKernelGGL((prefill_kernel<DT, 1>), grid, dim3(256), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((prefill_kernel<DT, 2>), grid, dim3(256), 0, stream, a); break;
     case 4: hipLaunchKernelGGL((prefill_kernel<DT, 4>), grid, dim3(256), 0, stream, a); break;
     default: hipLaunchKernelGGL((prefill_kernel<DT, 8>), grid, dim3(256), 0, stream, a); break;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  const int hq_total = a.kv_heads * group;
+  const dim3 cgrid(static_cast<unsigned>((a.q_len * hq_total + 7) / 8), static_cast<unsigned>(batch));
+  hipLaunchKernelGGL((prefill_combine_kernel<DT>), cgrid, dim3(256), 0, stream, a.o_part, a.lse_part, a.splits,
+                     a.q_len, hq_total, a.out, a.so_b, a.so_t, a.so_h);
   return hipGetLastError();
 }
 
@@ -442,10 +502,60 @@ void tile_geometry(int64_t q_len, int64_t n, int group, int64_t* nblk, int64_t* 
   *ntiles = (n + kKeys - 1) / kKeys;
 }
 
+constexpr int kMaxPrefillSplits = 16;
+constexpr int kMinSplitTiles = 4;    // keys per split: at least 256
+
+// Key splits of a call: 1 when the query blocks alone give every CU two
+// work-groups, else enough splits to do so (each at least kMinSplitTiles
+// tiles, at most kMaxPrefillSplits). requested > 0 overrides the choice.
+// Trailing empty splits are dropped: the result times its tiles covers n.
+int plan_splits(int batch, int64_t q_len, int64_t n, int group, int kv_heads, int requested, int64_t* split_tiles,
+                int* splits_out) {
+  int64_t nblk, ntiles;
+  tile_geometry(q_len, n, group, &nblk, &ntiles);
+  int64_t s = 1;
+  if (requested > 0) {
+    s = requested;
+  } else {
+    int cus = 0;
+    const int rc = current_device_cus(&cus);
+    if (rc != TC_OK) return rc;
+    const int64_t wgs = nblk * kv_heads * batch, slots = 2 * static_cast<int64_t>(cus);
+    if (wgs < slots) s = (slots + wgs - 1) / wgs;
+    s = std::min<int64_t>(s, std::max<int64_t>(1, ntiles / kMinSplitTiles));
+  }
+  s = std::max<int64_t>(1, std::min<int64_t>({s, kMaxPrefillSplits, std::max<int64_t>(1, ntiles)}));
+  const int64_t st = std::max<int64_t>(1, (ntiles + s - 1) / s);
+  *split_tiles = st;
+  *splits_out = static_cast<int>(std::max<int64_t>(1, (ntiles + st - 1) / st));
+  return TC_OK;
+}
+
+size_t workspace_bytes(int batch, int64_t q_len, int q_heads, int splits) {
+  if (splits <= 1) return 0;
+  return static_cast<size_t>(batch) * splits * q_len * q_heads * (kHeadDim + 1) * sizeof(float);
+}
+
 }  // namespace
 }  // namespace tc
 
 using namespace tc;
+
+extern "C" int tc_prefill_num_splits(int batch, int64_t q_len, int64_t n_tokens, int q_heads, int kv_heads) {
+  clear_error();
+  int group = 0, rc;
+  if (batch < 1 || q_len < 0 || n_tokens < q_len) return -fail(TC_ERR_INVALID_ARGUMENT, "batch %d, q_len %lld, n %lld", batch, (long long)q_len, (long long)n_tokens);
+  if ((rc = check_group(q_heads, kv_heads, &group)) != TC_OK) return -rc;
+  int64_t st;
+  int splits;
+  if ((rc = plan_splits(batch, q_len, n_tokens, group, kv_heads, 0, &st, &splits)) != TC_OK) return -rc;
+  return splits;
+}
+
+extern "C" size_t tc_prefill_workspace_bytes(int batch, int64_t q_len, int q_heads, int num_splits) {
+  if (batch < 1 || q_len < 0 || q_heads < 1) return 0;
+  return workspace_bytes(batch, q_len, q_heads, num_splits);
+}
 
 extern "C" size_t tc_prefill_tiles_bytes(int64_t q_len, int64_t n_tokens, int mask_batch, int q_heads,
                                          int kv_heads) {
@@ -491,8 +601,9 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
                                     const uint8_t* mask_dev, const int64_t mask_strides[3],
                                     const uint8_t* mask_tiles_dev, size_t mask_tiles_bytes, int causal,
                                     int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
-                                    int head_dim, int dtype, float scale, void* out_dev,
-                                    const int64_t out_strides[3], void* stream) {
+                                    int head_dim, int dtype, float scale, int num_splits, void* workspace_dev,
+                                    size_t workspace_bytes_in, void* out_dev, const int64_t out_strides[3],
+                                    void* stream) {
   clear_error();
   int group = 0, rc;
   if (batch < 1 || batch > 65535) return fail(TC_ERR_INVALID_ARGUMENT, "batch %d", batch);
@@ -518,7 +629,7 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
   if (!std::isfinite(scale)) return fail(TC_ERR_INVALID_ARGUMENT, "scale is not finite");
   int64_t nblk, ntiles;
   tile_geometry(q_len, n_tokens, group, &nblk, &ntiles);
-  if (nblk * kv_heads * batch > 0x7fffffff) return fail(TC_ERR_UNSUPPORTED, "grid too large");
+  if (nblk * kv_heads * batch * kMaxPrefillSplits > 0x7fffffff) return fail(TC_ERR_UNSUPPORTED, "grid too large");
   if (mask_dev) {
     if (causal) return fail(TC_ERR_INVALID_ARGUMENT, "pass either a mask or causal, not both");
     if ((rc = check_mask_strides(mask_strides)) != TC_OK) return rc;
@@ -531,7 +642,22 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
     return fail(TC_ERR_INVALID_ARGUMENT, "a tile map without its mask");
   }
 
+  int64_t split_tiles;
+  int splits;
+  if ((rc = plan_splits(batch, q_len, n_tokens, group, kv_heads, num_splits, &split_tiles, &splits)) != TC_OK)
+    return rc;
+  const size_t need = workspace_bytes(batch, q_len, q_heads, splits);
+  if (need > 0 && (!workspace_dev || workspace_bytes_in < need))
+    return fail(TC_ERR_WORKSPACE, "%d key splits need %zu workspace bytes, got %zu", splits, need,
+                workspace_dev ? workspace_bytes_in : size_t(0));
+  if (need > 0 && (reinterpret_cast<uintptr_t>(workspace_dev) & 15u))
+    return fail(TC_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+
   PrefillArgs a;
+  a.split_tiles = split_tiles;
+  a.splits = splits;
+  a.o_part = static_cast<float*>(workspace_dev);
+  a.lse_part = splits > 1 ? a.o_part + static_cast<size_t>(batch) * splits * q_len * q_heads * kHeadDim : nullptr;
   a.q = static_cast<const uint16_t*>(q_dev);
   a.k = static_cast<const uint16_t*>(k_dev);
   a.v = static_cast<const uint16_t*>(v_dev);

@@ -49,7 +49,15 @@ def _mask_strides(m):
     return st
 
 
-def prefill_attention(query, key, value, attention_mask=None, scale=None, is_causal=False, out=None):
+def num_splits(batch, q_len, n_tokens, q_heads, kv_heads):
+    """Key splits a call of this size uses (1 when the query blocks fill the GPU)."""
+    s = _lib.load().tc_prefill_num_splits(int(batch), int(q_len), int(n_tokens), int(q_heads), int(kv_heads))
+    if s < 0:
+        _lib.check(-s, "tc_prefill_num_splits")
+    return s
+
+
+def prefill_attention(query, key, value, attention_mask=None, scale=None, is_causal=False, out=None, splits=None):
     """SDPA(query, repeat_kv(key, g), repeat_kv(value, g), attention_mask, scale,
     is_causal).transpose(1, 2) without expanding K/V.
 
@@ -58,6 +66,8 @@ def prefill_attention(query, key, value, attention_mask=None, scale=None, is_cau
     ``is_causal`` needs no mask and aligns the queries to the end of the keys
     (identical to SDPA's when q == n). Returns out [b, q, hq, d] (a new
     contiguous tensor unless `out` is given). Rows with no visible key are 0.
+    ``splits`` fixes the number of key splits (default: ``num_splits``); more
+    than one adds a workspace of fp32 partials and a combine pass.
     """
     _lib.require_gpu(query, key, value, what="prefill_attention")
     if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
@@ -91,12 +101,16 @@ def prefill_attention(query, key, value, attention_mask=None, scale=None, is_cau
         mask_ptr, mask_strides = m.data_ptr(), _mask_strides(m)
     scale = scale if scale is not None else d ** -0.5
     lib = _lib.load()
+    s = int(splits) if splits else num_splits(b, q, n, hq, hkv)
+    ws_bytes = lib.tc_prefill_workspace_bytes(b, q, hq, s)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes else None
     rc = lib.tc_prefill_attention(
         query.data_ptr(), _strides(query, (0, 1, 2)), key.data_ptr(), _strides(key, (0, 1, 2), 2),
         value.data_ptr(), _strides(value, (0, 1, 2), 2), mask_ptr, mask_strides,
         None if tiles is None else tiles.data_ptr(), 0 if tiles is None else tiles.numel(), int(bool(is_causal)),
-        q, n, b, hq, hkv, d, _lib.dtype_code(query.dtype), float(scale),
-        out.data_ptr(), _strides(out, (0, 1, 2)), _lib.stream_of(query.device))
+        q, n, b, hq, hkv, d, _lib.dtype_code(query.dtype), float(scale), s,
+        None if ws is None else ws.data_ptr(), ws_bytes, out.data_ptr(), _strides(out, (0, 1, 2)),
+        _lib.stream_of(query.device))
     _lib.check(rc, "tc_prefill_attention")
     return out
 
