@@ -16,7 +16,11 @@ Printed JSON line:
   heads folded, fp16, threadcut/attention.py:40-42) on the host cores;
 - splice: the 36-layer suffix splice (Split(2048, 8668, 5668), 14336-token
   caches, theta 1e6) in one launch, algorithmic GB/s (C of K and V read and
-  written).
+  written);
+- prefill: the GQA-native prefill attention on a 2048-token chunk over the
+  7716 tokens that splice keeps, a 300-token chunk over 9700, and a causal
+  2048-token prompt, in TFLOP/s of the matrix cores next to the reference's
+  GPU route (repeat_kv + SDPA).
 """
 import argparse
 import json
@@ -286,6 +290,65 @@ def measure_append(dev, n, steps):
             "us_per_layer_fused_append": round(ms_fused * 1e3 / LAYERS, 3)}
 
 
+PEAK_MFMA_F16 = 2500.0  # dense fp16 matrix-core TFLOP/s of one MI355X
+
+
+def prefill_flops(q_len, n, causal_like, hq=HQ, d=D):
+    """Algorithmic FLOPs of one prefill attention call: 2*d each for QK^T and PV per
+    visible (query head, query, key) triple; a causal chunk sees n - q_len + t + 1 keys."""
+    pairs = q_len * n - (q_len * (q_len - 1) // 2 if causal_like else 0)
+    return 4 * pairs * d * hq
+
+
+def measure_prefill(dev, steps):
+    """Prefill attention at the Qwen3-4B shape (32 q / 8 kv heads, D=128, fp16): the
+    GQA-native kernel vs the reference's GPU route (repeat_kv + SDPA with the same mask)."""
+    import torch
+
+    from threadcut_amd import attention, prefill, workloads
+
+    def timed(fn, iters):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters * 1e3
+
+    cases = [("chunk_2048_on_7716", workloads.PREFILL_CHUNK, workloads.PREFILL_PAST + workloads.PREFILL_CHUNK, True),
+             ("chunk_300_on_9700", 300, 10000, True),
+             ("prompt_2048_causal", 2048, 2048, False)]
+    out = {}
+    for name, L, n, masked in cases:
+        q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, device=dev)
+        mask = workloads.causal_mask(L, n, device=dev) if masked else None
+        causal = not masked
+        scale = D ** -0.5
+        iters = max(5, steps // 10)
+        prefill.prefill_attention(q, k, v, mask, scale, causal)  # builds the mask's tile map once
+        us = timed(lambda: prefill.prefill_attention(q, k, v, mask, scale, causal), iters)
+        ref = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
+            q, attention.repeat_kv(k, HQ // HKV), attention.repeat_kv(v, HQ // HKV), attn_mask=mask, scale=scale,
+            is_causal=causal).transpose(1, 2).contiguous(), iters)
+        tflops = prefill_flops(L, n, True) / (us * 1e-6) / 1e12
+        r = {"q_len": L, "kv_tokens": n, "mask": "bool [1,1,q,n] causal" if masked else "is_causal",
+             "splits": prefill.num_splits(1, L, n, HQ, HKV), "us_per_call": round(us, 1),
+             "tflops": round(tflops, 1), "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16, 4),
+             "reference_route_us": round(ref, 1), "speedup": round(ref / us, 2)}
+        if masked:
+            prefill._tile_cache = None
+            r["mask_tile_map_us_once_per_forward"] = round(timed(
+                lambda: (setattr(prefill, "_tile_cache", None), prefill.mask_tiles(mask, HQ, HKV)), iters), 1)
+        out[name] = r
+        del q, k, v, mask
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_match(seconds=2.0):
     """Request split at a 131072-token cache: the native matcher vs the reference's numpy windows."""
     import numpy as np
@@ -325,7 +388,7 @@ def main():
     ap.add_argument("--no-splice", action="store_true")
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
-    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy", "prefill"], default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
     args = ap.parse_args()
@@ -346,6 +409,9 @@ def main():
 
     if args.only == "splice":
         print(json.dumps(bench_splice(dev, args.steps, args.warmup)))
+        return
+    if args.only == "prefill":
+        print(json.dumps(measure_prefill(dev, args.steps)))
         return
     if args.only == "copy":
         src = torch.empty(128 << 20, dtype=torch.float16, device=dev).normal_()
@@ -402,6 +468,7 @@ def main():
         line["long_131072"] = {f"B{b}": measure_long(dev, b, max(10, args.steps // 10)) for b in (1, 4)}
         line["decode_append"] = measure_append(dev, n, max(20, args.steps // 4))
         line["match_split"] = measure_match()
+        line["prefill"] = measure_prefill(dev, args.steps)
     if not args.no_splice:
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:
