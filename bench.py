@@ -349,6 +349,68 @@ def measure_prefill(dev, steps):
     return out
 
 
+QWEN3_4B_CONFIG = dict(vocab_size=151936, hidden_size=2560, intermediate_size=9728, num_hidden_layers=LAYERS,
+                       num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=D, max_position_embeddings=40960,
+                       rope_theta=1e6, tie_word_embeddings=True)
+
+
+def measure_decode_step(dev, n=10240, steps=40):
+    """Whole-model decode step at the Qwen3-4B shape (random fp16 weights, 36 layers) at n
+    cached tokens: the reference's eager per-token loop (engine.py:88-95) with the "threadcut"
+    attention and fused cache append, against the same step captured once and replayed
+    (graph.DecodeGraph)."""
+    import torch
+    from transformers import AutoModelForCausalLM, Qwen3Config
+
+    from threadcut_amd import attention, kv
+    from threadcut_amd.graph import DecodeGraph
+
+    torch.manual_seed(8)
+    cfg = Qwen3Config(**QWEN3_4B_CONFIG)
+    with torch.device(dev):
+        model = AutoModelForCausalLM.from_config(cfg, dtype=torch.float16, attn_implementation=attention.NAME)
+    model.eval()
+    g = torch.Generator(device=dev)
+    g.manual_seed(8)
+    prompt = torch.randint(0, cfg.vocab_size, (1, n), generator=g, device=dev)
+    caches = [kv.new_cache(cfg, fused_append=True) for _ in range(2)]
+    with torch.no_grad():
+        for c in caches:
+            for i in range(0, n, 2048):
+                model(input_ids=prompt[:, i:i + 2048], past_key_values=c, use_cache=True, logits_to_keep=1)
+        tok = torch.randint(0, cfg.vocab_size, (1, 1), generator=g, device=dev)
+
+        def eager_step():
+            return model(input_ids=tok, past_key_values=caches[0], use_cache=True, logits_to_keep=1).logits
+
+        for _ in range(3):
+            eager_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eager_step()
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+        dg = DecodeGraph(model, caches[1], max_new_tokens=steps + 8)
+        for _ in range(3):
+            dg.step(tok)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dg.step(tok)
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - t0) * 1e3 / steps
+        dg.close()
+    weights = sum(p.numel() * p.element_size() for p in model.parameters())
+    del model, caches, dg
+    torch.cuda.empty_cache()
+    return {"kv_tokens": n, "layers": LAYERS, "weights_GB": round(weights / 1e9, 2),
+            "eager_ms_per_token": round(eager_ms, 3), "graph_ms_per_token": round(graph_ms, 3),
+            "speedup": round(eager_ms / graph_ms, 2),
+            "graph_weight_read_GB/s": round(weights / (graph_ms * 1e-3) / 1e9, 1),
+            "note": "random-init weights; the step includes every layer's projections, MLP and the LM head"}
+
+
 def measure_match(seconds=2.0):
     """Request split at a 131072-token cache: the native matcher vs the reference's numpy windows."""
     import numpy as np
@@ -388,7 +450,8 @@ def main():
     ap.add_argument("--no-splice", action="store_true")
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
-    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy", "prefill"], default=None,
+    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy", "prefill", "decode-step"],
+                    default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
     args = ap.parse_args()
@@ -412,6 +475,9 @@ def main():
         return
     if args.only == "prefill":
         print(json.dumps(measure_prefill(dev, args.steps)))
+        return
+    if args.only == "decode-step":
+        print(json.dumps(measure_decode_step(dev, args.n)))
         return
     if args.only == "copy":
         src = torch.empty(128 << 20, dtype=torch.float16, device=dev).normal_()
@@ -469,6 +535,7 @@ def main():
         line["decode_append"] = measure_append(dev, n, max(20, args.steps // 4))
         line["match_split"] = measure_match()
         line["prefill"] = measure_prefill(dev, args.steps)
+        line["decode_step_model"] = measure_decode_step(dev, n)
     if not args.no_splice:
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:

@@ -141,6 +141,29 @@ int tc_decode_append_attention(const void* q_dev, const int64_t q_strides[3],
                                void* workspace_dev, size_t workspace_bytes,
                                void* out_dev, const int64_t out_strides[3], void* stream);
 
+/* tc_decode_append_attention with the append position on the device, so a
+ * captured HIP graph of the decode step replays correctly while the cache
+ * grows: for sequence b the new token's K/V row is written to row pos[b] of
+ * k_cache / v_cache ([B, Hkv, capacity, D] buffers) and the query attends rows
+ * [0, pos[b]] (pos[b] cached tokens, then the new one). pos[b] is clamped to
+ * [0, capacity - 1]; the caller advances pos (e.g. a kernel in the same graph)
+ * and stops before the buffers are full. The split plan and workspace are
+ * those of tc_decode_attention(..., n_tokens = capacity, lens = NULL). This is
+ * the device-side form of GrowingLayer.update + decode attention
+ * (threadcut/kv.py:68-77, threadcut/attention.py:35-39) that the engine's
+ * per-token loop (threadcut/engine.py:88-95) needs for graph capture; the
+ * reference has no counterpart. */
+int tc_decode_append_attention_at(const void* q_dev, const int64_t q_strides[3],
+                                  void* k_cache_dev, const int64_t k_strides[3],
+                                  void* v_cache_dev, const int64_t v_strides[3],
+                                  const void* k_new_dev, const int64_t k_new_strides[2],
+                                  const void* v_new_dev, const int64_t v_new_strides[2],
+                                  const int32_t* pos_dev, int64_t capacity,
+                                  int batch, int kv_heads, int group, int head_dim, int dtype,
+                                  float scale, int split_tokens,
+                                  void* workspace_dev, size_t workspace_bytes,
+                                  void* out_dev, const int64_t out_strides[3], void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* RoPE delta-shift and suffix splice                                        */
 /*                                                                           */

@@ -16,7 +16,7 @@ from transformers import AttentionInterface
 from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 
 from . import kv, prefill
-from .flash_decode import decode_append_into, decode_into
+from .flash_decode import decode_append_at, decode_append_into, decode_into
 
 NAME = "threadcut"
 
@@ -47,8 +47,12 @@ def attention(module, query, key, value, attention_mask, dropout=0.0, scaling=No
             # GrowingLayer deferred this token's append: write it and attend in one launch.
             k_new, v_new = layer.pending
             layer.pending = None
-            decode_append_into(query.reshape(b, hkv, g, d), layer.kbuf, layer.vbuf, k_new, v_new, layer.n,
-                               scaling, out.view(b, hkv, g, d))
+            if layer.device_pos is not None:  # graph-captured step: the position lives on the device
+                decode_append_at(query.reshape(b, hkv, g, d), layer.kbuf, layer.vbuf, k_new, v_new,
+                                 layer.device_pos, scaling, out.view(b, hkv, g, d))
+            else:
+                decode_append_into(query.reshape(b, hkv, g, d), layer.kbuf, layer.vbuf, k_new, v_new, layer.n,
+                                   scaling, out.view(b, hkv, g, d))
         else:
             decode_into(query.reshape(b, hkv, g, d), key, value, scaling, out.view(b, hkv, g, d))
         return out, None

@@ -345,10 +345,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   const int h = blockIdx.y;
   const int b = blockIdx.z;
 
-  // Lengths past the buffer (or negative) are clamped into [0, n]; with an
-  // append, the last of the n tokens comes from k_new/v_new, not the cache.
-  const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), a.n)
-                             : (a.k_new ? a.n - 1 : a.n);
+  // Cached tokens attended. Lengths past the buffer (or negative) are clamped
+  // into [0, n]. With an append the new token is one more, read from
+  // k_new/v_new and written to row `len`, so len stays below n: n - 1
+  // without lengths, lens[b] (the append position) clamped to n - 1 with.
+  const int64_t len_cap = a.k_new ? a.n - 1 : a.n;
+  const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), len_cap) : len_cap;
   // The wave's 16-token tiles: first, first + stride, ... with tokens < end.
   // Contiguous: split s, wave w own [s*T + w*T/W, s*T + (w+1)*T/W). Interleaved:
   // all S*W waves of a head sweep the cache together, wave g taking tiles
@@ -834,12 +836,12 @@ int attention_impl(const void* q_dev, const int64_t q_strides[3], const void* k_
                    const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
                    int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
                    void* workspace_dev, size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
-                   const Append* app, void* stream) {
+                   const Append* app, int ragged_plan, void* stream) {
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
   int S = 0, t = 0;
-  if ((rc = split_plan(batch, kv_heads, n_tokens, split_tokens, lens_dev != nullptr, &S, &t)) != TC_OK) return rc;
+  if ((rc = split_plan(batch, kv_heads, n_tokens, split_tokens, ragged_plan, &S, &t)) != TC_OK) return rc;
   const size_t need = tc_decode_workspace_bytes(batch, kv_heads, group, head_dim, S);
   if (S > 0 && (!workspace_dev || workspace_bytes < need))
     return fail(TC_ERR_WORKSPACE, "workspace of %zu bytes, %zu needed for %d splits", workspace_bytes, need, S);
@@ -867,16 +869,15 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const voi
   clear_error();
   return attention_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads,
                         group, head_dim, dtype, scale, split_tokens, workspace_dev, workspace_bytes, out_dev,
-                        out_strides, nullptr, stream);
+                        out_strides, nullptr, lens_dev != nullptr, stream);
 }
 
-int tc_decode_append_attention(const void* q_dev, const int64_t q_strides[3], void* k_cache_dev,
-                               const int64_t k_strides[3], void* v_cache_dev, const int64_t v_strides[3],
-                               const void* k_new_dev, const int64_t k_new_strides[2], const void* v_new_dev,
-                               const int64_t v_new_strides[2], int64_t n_tokens, int batch, int kv_heads, int group,
-                               int head_dim, int dtype, float scale, int split_tokens, void* workspace_dev,
-                               size_t workspace_bytes, void* out_dev, const int64_t out_strides[3], void* stream) {
-  clear_error();
+static int append_impl(const void* q_dev, const int64_t q_strides[3], void* k_cache_dev, const int64_t k_strides[3],
+                       void* v_cache_dev, const int64_t v_strides[3], const void* k_new_dev,
+                       const int64_t k_new_strides[2], const void* v_new_dev, const int64_t v_new_strides[2],
+                       const int32_t* pos_dev, int64_t n_tokens, int batch, int kv_heads, int group, int head_dim,
+                       int dtype, float scale, int split_tokens, void* workspace_dev, size_t workspace_bytes,
+                       void* out_dev, const int64_t out_strides[3], void* stream) {
   if (n_tokens < 1) return fail(TC_ERR_INVALID_ARGUMENT, "append needs n_tokens >= 1 (got %lld)", (long long)n_tokens);
   if (!k_new_dev || !v_new_dev || !k_new_strides || !v_new_strides)
     return fail(TC_ERR_INVALID_ARGUMENT, "null new-token K/V");
@@ -886,9 +887,35 @@ int tc_decode_append_attention(const void* q_dev, const int64_t q_strides[3], vo
     if (k_new_strides[i] < 0 || v_new_strides[i] < 0 || k_new_strides[i] % 8 || v_new_strides[i] % 8)
       return fail(TC_ERR_ALIGNMENT, "new-token K/V strides must be non-negative multiples of 8");
   const Append app{k_new_dev, k_new_strides, v_new_dev, v_new_strides, k_cache_dev, v_cache_dev};
-  return attention_impl(q_dev, q_strides, k_cache_dev, k_strides, v_cache_dev, v_strides, nullptr, n_tokens, batch,
+  return attention_impl(q_dev, q_strides, k_cache_dev, k_strides, v_cache_dev, v_strides, pos_dev, n_tokens, batch,
                         kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev, workspace_bytes, out_dev,
-                        out_strides, &app, stream);
+                        out_strides, &app, 0, stream);
+}
+
+int tc_decode_append_attention(const void* q_dev, const int64_t q_strides[3], void* k_cache_dev,
+                               const int64_t k_strides[3], void* v_cache_dev, const int64_t v_strides[3],
+                               const void* k_new_dev, const int64_t k_new_strides[2], const void* v_new_dev,
+                               const int64_t v_new_strides[2], int64_t n_tokens, int batch, int kv_heads, int group,
+                               int head_dim, int dtype, float scale, int split_tokens, void* workspace_dev,
+                               size_t workspace_bytes, void* out_dev, const int64_t out_strides[3], void* stream) {
+  clear_error();
+  return append_impl(q_dev, q_strides, k_cache_dev, k_strides, v_cache_dev, v_strides, k_new_dev, k_new_strides,
+                     v_new_dev, v_new_strides, nullptr, n_tokens, batch, kv_heads, group, head_dim, dtype, scale,
+                     split_tokens, workspace_dev, workspace_bytes, out_dev, out_strides, stream);
+}
+
+int tc_decode_append_attention_at(const void* q_dev, const int64_t q_strides[3], void* k_cache_dev,
+                                  const int64_t k_strides[3], void* v_cache_dev, const int64_t v_strides[3],
+                                  const void* k_new_dev, const int64_t k_new_strides[2], const void* v_new_dev,
+                                  const int64_t v_new_strides[2], const int32_t* pos_dev, int64_t capacity,
+                                  int batch, int kv_heads, int group, int head_dim, int dtype, float scale,
+                                  int split_tokens, void* workspace_dev, size_t workspace_bytes, void* out_dev,
+                                  const int64_t out_strides[3], void* stream) {
+  clear_error();
+  if (!pos_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null append positions");
+  return append_impl(q_dev, q_strides, k_cache_dev, k_strides, v_cache_dev, v_strides, k_new_dev, k_new_strides,
+                     v_new_dev, v_new_strides, pos_dev, capacity, batch, kv_heads, group, head_dim, dtype, scale,
+                     split_tokens, workspace_dev, workspace_bytes, out_dev, out_strides, stream);
 }
 
 }  // extern "C"

@@ -128,6 +128,44 @@ def decode_append_into(q, k_cache, v_cache, k_new, v_new, n, scale, out, split=N
     return out
 
 
+def decode_append_at(q, k_cache, v_cache, k_new, v_new, pos, scale, out, split=None):
+    """decode_append_into with the append position on the device (graph-capturable).
+
+    pos: int32 [B] on the device, the number of tokens already cached per
+    sequence: the new rows go to token pos[b] of k_cache/v_cache [B,Hkv,cap,D]
+    and q attends over tokens [0, pos[b]]. Nothing here reads pos on the host,
+    so a captured graph of this call stays valid while pos advances. The split
+    plan depends on cap only.
+    """
+    _check_qkv(q, k_cache, v_cache, "decode_append_at")
+    b, hkv, g, d = q.shape
+    kn = k_new.reshape(b, hkv, d) if k_new.dim() == 4 else k_new
+    vn = v_new.reshape(b, hkv, d) if v_new.dim() == 4 else v_new
+    _lib.require_gpu(kn, vn, out, pos, what="decode_append_at")
+    if kn.shape != (b, hkv, d) or vn.shape != (b, hkv, d) or kn.dtype != q.dtype or vn.dtype != q.dtype:
+        raise ValueError("decode_append_at: new K/V must be [B, Hkv, D] in the query dtype")
+    if kn.stride(2) != 1 or vn.stride(2) != 1:
+        raise ValueError("decode_append_at: new K/V need a contiguous last dimension")
+    if pos.dtype != torch.int32 or pos.shape != (b,) or not pos.is_contiguous() or pos.device != q.device:
+        raise ValueError("decode_append_at: pos must be a contiguous int32 [B] tensor on the device")
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(3) != 1:
+        raise ValueError("decode_append_at: out must match q")
+    cap = k_cache.shape[2]
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        s = num_splits(b, hkv, cap, split)
+        nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+        st2 = lambda t: _lib.i64x2(t.stride(0) if t.shape[0] > 1 else 0, t.stride(1) if t.shape[1] > 1 else 0)
+        rc = lib.tc_decode_append_attention_at(
+            q.data_ptr(), _strides3(q), k_cache.data_ptr(), _strides3(k_cache, True), v_cache.data_ptr(),
+            _strides3(v_cache, True), kn.data_ptr(), st2(kn), vn.data_ptr(), st2(vn), pos.data_ptr(), int(cap),
+            b, hkv, g, d, _lib.dtype_code(q.dtype), float(scale), int(split or 0),
+            ws.data_ptr(), ws.numel(), out.data_ptr(), _strides3(out), _lib.stream_of(q.device))
+        _lib.check(rc, "tc_decode_append_attention_at")
+    return out
+
+
 def decode_attention_batched(q, k, v, scale, lens=None, split=None):
     """Batched form: q [B,Hkv,G,D], k/v [B,Hkv,N,D] → [B,Hkv,G,D] in q.dtype."""
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)

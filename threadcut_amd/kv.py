@@ -184,6 +184,10 @@ class GrowingLayer(DynamicLayer):
 
     fused_append = False
     pending = None
+    # Set by graph.DecodeGraph: an int32 [B] device tensor holding the token
+    # count, so the decode kernel takes the append position from the device
+    # (tc_decode_append_attention_at) instead of from the host-side n.
+    device_pos = None
 
     def lazy_initialization(self, key_states, value_states):
         super().lazy_initialization(key_states, value_states)
@@ -219,7 +223,7 @@ class GrowingLayer(DynamicLayer):
         self.flush()
         add = key_states.shape[-2]
         self._reserve(self.n + add, key_states)
-        if self.fused_append and add == 1 and key_states.is_cuda:
+        if (self.fused_append or self.device_pos is not None) and add == 1 and key_states.is_cuda:
             self.pending = (key_states, value_states)
             _PENDING[self.kbuf.data_ptr()] = self
         else:
