@@ -154,10 +154,12 @@ __device__ __forceinline__ void store_stage(const Stage& s, uint16_t* lk, uint16
   const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&s.v[3]);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int sh = (e & 1) * 16;
-    const uint32_t x0 = (w0[e >> 1] >> sh) & 0xffffu, x1 = (w1[e >> 1] >> sh) & 0xffffu;
-    const uint32_t x2 = (w2[e >> 1] >> sh) & 0xffffu, x3 = (w3[e >> 1] >> sh) & 0xffffu;
-    *reinterpret_cast<uint2*>(lv + (8 * dc + e) * kVStride + 4 * kq) = make_uint2(x0 | (x1 << 16), x2 | (x3 << 16));
+    // Element e of rows 0/1 and of rows 2/3 into one word each (v_perm_b32:
+    // low halves 0x05040100, high halves 0x07060302).
+    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+    const uint32_t x01 = __builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel);
+    const uint32_t x23 = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);
+    *reinterpret_cast<uint2*>(lv + (8 * dc + e) * kVStride + 4 * kq) = make_uint2(x01, x23);
   }
 }
 
@@ -171,6 +173,15 @@ __device__ __forceinline__ float pair_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+
+// The running maximum moves only when a tile's maximum exceeds it by more
+// than this (log2 units), so p = exp2(s*c - m) <= 2^kLazy.
+constexpr float kLazy = 8.f;
+
+// (1, 1) as two 16-bit elements: dot2(p, kOnes) is the sum of a packed pair.
+template <int DT> constexpr uint32_t kOnes = 0;
+template <> constexpr uint32_t kOnes<TC_DTYPE_F16> = 0x3C003C00u;
+template <> constexpr uint32_t kOnes<TC_DTYPE_BF16> = 0x3F803F80u;
 
 // Key offset (within a 32-key half) of accumulator v of a lane in half `hi`.
 __device__ __forceinline__ int acc_key(int v, int hi) { return 8 * (v >> 2) + 4 * hi + (v & 3); }
@@ -269,81 +280,88 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
     const uint16_t* lk = s_k[buf];
     const uint16_t* lv = s_v[buf];
-    const int64_t key0 = t * kKeys;
-    // Visible-key limit of this lane's row on a MIXED tile (keys of the tile below it).
-    int lim = kKeys;
-    const uint8_t* mt = nullptr;
-    if (cls == TILE_MIXED) {
-      int64_t lim64 = a.n - key0;
-      if (a.causal) lim64 = min(lim64, past + tok + 1 - key0);
-      lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
-      mt = mrow ? mrow + key0 : nullptr;
-    }
 
-    // The tile in two 32-key halves, each a full online-softmax step.
+    // S^T of the tile: two 32-key halves as two independent MFMA chains.
+    float16v s[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      float16v s;
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) s[v] = 0.f;
+      for (int v = 0; v < 16; ++v) s[kt][v] = 0.f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
         const uint4 ka = *reinterpret_cast<const uint4*>(lk + (32 * kt + r32) * kKStride + 16 * c + 8 * hi);
-        s = Mfma<DT>::mma(ka, qb[c], s);
+        s[kt] = Mfma<DT>::mma(ka, qb[c], s[kt]);
       }
 
-      // Visible keys of this lane (bit v), all of them on a FULL tile.
-      uint32_t vis = 0xffffu;
-      if (cls == TILE_MIXED) {
-        vis = 0;
+    // Visible keys of this lane (bit 16*kt + v), all of them on a FULL tile.
+    uint32_t vis = 0xffffffffu;
+    float mx = neg_inf();
+    if (cls == TILE_MIXED) {
+      const int64_t key0 = t * kKeys;
+      int64_t lim64 = a.n - key0;
+      if (a.causal) lim64 = min(lim64, past + tok + 1 - key0);
+      const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
+      const uint8_t* mt = mrow ? mrow + key0 : nullptr;
+      vis = 0;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = 32 * kt + acc_key(v, hi);
           bool ok = key < lim;
           if (mt && ok) ok = mt[key] != 0;
-          vis |= ok ? (1u << v) : 0u;
+          vis |= ok ? (1u << (16 * kt + v)) : 0u;
         }
-      }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, (vis >> (16 * kt + v)) & 1u ? s[kt][v] : neg_inf());
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
+    }
 
-      // Row maximum of the raw scores (c >= 0, so max(s * c) = c * max(s)).
-      float mx = neg_inf();
-      if (cls == TILE_MIXED) {
+    // Running maximum, moved only when the tile's maximum exceeds it by more
+    // than 2^kLazy: p = exp2(s*c - m) then stays below 2^kLazy (exact in
+    // fp16/bf16 range) and the accumulators are rescaled rarely.
+    mx = pair_max(mx);
+    const float tmax = mx == neg_inf() ? neg_inf() : mx * a.c;
+    const bool move = tmax > m + kLazy;
+    const float mn = move ? tmax : m;
+    const float alpha = move ? __builtin_amdgcn_exp2f(m - mn) : 1.f;
+    m = mn;
+    const float ms = (m == neg_inf()) ? 0.f : m;
+    if (__builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, (vis >> v) & 1u ? s[v] : neg_inf());
-      } else {
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
-      }
-      mx = pair_max(mx);
-      const float mn = fmaxf(m, mx == neg_inf() ? neg_inf() : mx * a.c);
-      const float ms = (mn == neg_inf()) ? 0.f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m - ms);
-      m = mn;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) o[dt][v] *= alpha;
-      }
+        for (int v = 0; v < 16; ++v) o[dt][v] *= alpha;
+      l *= alpha;
+    }
 
-      // P^T operand of chunk c2: accumulators 8*c2 .. 8*c2+7 are keys
-      // 16*c2 + {4hi..4hi+3, 8+4hi..8+4hi+3} of the half, the order in which
-      // V^T is read.
-      float psum = 0.f;
+    // P^T operand of half kt, chunk c2: accumulators 8*c2 .. 8*c2+7 are keys
+    // 16*c2 + {4hi..4hi+3, 8+4hi..8+4hi+3} of the half, the order in which V^T
+    // is read. The row sum takes the rounded P, as the MFMA does.
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2) {
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int v0 = 8 * c2 + 2 * j;
-          float p0 = __builtin_amdgcn_exp2f(fmaf(s[v0], a.c, -ms));
-          float p1 = __builtin_amdgcn_exp2f(fmaf(s[v0 + 1], a.c, -ms));
+          float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][v0], a.c, -ms));
+          float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][v0 + 1], a.c, -ms));
           if (cls == TILE_MIXED) {
-            p0 = (vis >> v0) & 1u ? p0 : 0.f;
-            p1 = (vis >> (v0 + 1)) & 1u ? p1 : 0.f;
+            p0 = (vis >> (16 * kt + v0)) & 1u ? p0 : 0.f;
+            p1 = (vis >> (16 * kt + v0 + 1)) & 1u ? p1 : 0.f;
           }
-          psum += p0 + p1;
           w[j] = pack2<DT>(p0, p1);
+          l = Elem<DT>::dot2(w[j], kOnes<DT>, l);
         }
         const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
 #pragma unroll
@@ -354,8 +372,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
           o[dt] = Mfma<DT>::mma(make_uint4(lo.x, lo.y, up.x, up.y), pb, o[dt]);
         }
       }
-      l = l * alpha + psum;
-    }
 
     if (more) store_stage(st, s_k[buf ^ 1], s_v[buf ^ 1]);
     __syncthreads();
