@@ -37,7 +37,13 @@ namespace tc {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kRows = 128;         // query rows per work-group (4 waves x 32)
+// Row groups of 32 query rows per wave: each K/V fragment read from LDS
+// feeds that many MFMAs.
+#ifndef TC_PREFILL_GROUPS
+#define TC_PREFILL_GROUPS 1
+#endif
+constexpr int kGroups = TC_PREFILL_GROUPS;
+constexpr int kRows = 4 * 32 * kGroups;  // query rows per work-group (4 waves)
 constexpr int kKeys = 64;          // keys per tile
 constexpr int kKStride = 136;      // halfs per K row in LDS (256 B + 16 B pad)
 constexpr int kVStride = 68;       // halfs per V^T row in LDS (128 B + 8 B pad)
@@ -196,7 +202,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hi = lane >> 5;            // which 16 keys of each 32-key half this lane holds
-  const int r32 = lane & 31;           // the lane's query row within the wave
+  const int r32 = lane & 31;           // the lane's query row within each 32-row group
 
   // Work item (KV head fastest, then key split, query block, batch):
   // consecutive work-groups go to different XCDs round-robin, so with
@@ -210,31 +216,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const int b = static_cast<int>(rest / a.nblk);
   if (a.causal) blk = a.nblk - 1 - blk;  // longest rows first
   const int64_t tok0 = blk * kTokens;
-
-  const int row = wave * 32 + r32;
-  const int64_t tok = tok0 + row / G;
-  const int hq = h * G + row % G;
-  const bool row_ok = tok < a.q_len;
   const int64_t past = a.n - a.q_len;
+  const int64_t bm = a.sm_b ? b : 0;
 
-  // Q^T as the MFMA B operand: dims 16c + 8*hi .. +8 of this lane's row.
-  uint4 qb[8];
-  {
-    const uint16_t* qp = a.q + b * a.sq_b + hq * a.sq_h + (row_ok ? tok : 0) * a.sq_t + 8 * hi;
+  // The wave's kGroups row groups of 32 rows: row = (token, head of the group).
+  int64_t tok[kGroups];
+  int hq[kGroups];
+  bool row_ok[kGroups];
+  const uint8_t* mrow[kGroups];
+  uint4 qb[kGroups][8];  // Q^T as the MFMA B operand: dims 16c + 8*hi .. +8 of the lane's row
+#pragma unroll
+  for (int rg = 0; rg < kGroups; ++rg) {
+    const int row = (wave * kGroups + rg) * 32 + r32;
+    tok[rg] = tok0 + row / G;
+    hq[rg] = h * G + row % G;
+    row_ok[rg] = tok[rg] < a.q_len;
+    mrow[rg] = a.mask ? a.mask + bm * a.sm_b + (row_ok[rg] ? tok[rg] : 0) * a.sm_q : nullptr;
+    const uint16_t* qp = a.q + b * a.sq_b + hq[rg] * a.sq_h + (row_ok[rg] ? tok[rg] : 0) * a.sq_t + 8 * hi;
     const uint32_t flip = a.neg ? 0x80008000u : 0u;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      uint4 x = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * c) : make_uint4(0u, 0u, 0u, 0u);
+      uint4 x = row_ok[rg] ? *reinterpret_cast<const uint4*>(qp + 16 * c) : make_uint4(0u, 0u, 0u, 0u);
       x.x ^= flip; x.y ^= flip; x.z ^= flip; x.w ^= flip;
-      qb[c] = x;
+      qb[rg][c] = x;
     }
   }
 
   const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
   const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
   const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
-  const int64_t bm = a.sm_b ? b : 0;
-  const uint8_t* mrow = a.mask ? a.mask + bm * a.sm_b + (row_ok ? tok : 0) * a.sm_q : nullptr;
   const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.ntiles : nullptr;
 
   // Tiles this work-group may need: its split's share of all n keys, cut at
@@ -256,12 +266,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     return t;
   };
 
-  float m = neg_inf(), l = 0.f;
-  float16v o[4];
+  float m[kGroups], l[kGroups];
+  float16v o[kGroups][4];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int rg = 0; rg < kGroups; ++rg) {
+    m[rg] = neg_inf();
+    l[rg] = 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) o[dt][v] = 0.f;
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[rg][dt][v] = 0.f;
+  }
 
   Stage st;
   int64_t t = next_active(t_begin);
@@ -277,101 +292,116 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     const bool more = tn < nt;
     if (more) load_stage(st, kslab, vslab, row_k, row_v, tn * kKeys, a.n);
     const int cls = tile_class(t);
-
     const uint16_t* lk = s_k[buf];
     const uint16_t* lv = s_v[buf];
 
-    // S^T of the tile: two 32-key halves as two independent MFMA chains.
-    float16v s[2];
+    // S^T of the tile for every row group: each K fragment read from LDS
+    // feeds kGroups MFMAs; the two 32-key halves are independent chains.
+    float16v s[kGroups][2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int rg = 0; rg < kGroups; ++rg)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) s[kt][v] = 0.f;
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[rg][kt][v] = 0.f;
 #pragma unroll
     for (int c = 0; c < 8; ++c)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         const uint4 ka = *reinterpret_cast<const uint4*>(lk + (32 * kt + r32) * kKStride + 16 * c + 8 * hi);
-        s[kt] = Mfma<DT>::mma(ka, qb[c], s[kt]);
+#pragma unroll
+        for (int rg = 0; rg < kGroups; ++rg) s[rg][kt] = Mfma<DT>::mma(ka, qb[rg][c], s[rg][kt]);
       }
 
-    // Visible keys of this lane (bit 16*kt + v), all of them on a FULL tile.
-    uint32_t vis = 0xffffffffu;
-    float mx = neg_inf();
-    if (cls == TILE_MIXED) {
-      const int64_t key0 = t * kKeys;
-      int64_t lim64 = a.n - key0;
-      if (a.causal) lim64 = min(lim64, past + tok + 1 - key0);
-      const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
-      const uint8_t* mt = mrow ? mrow + key0 : nullptr;
-      vis = 0;
+    uint4 pb[kGroups][2][2];
+#pragma unroll
+    for (int rg = 0; rg < kGroups; ++rg) {
+      // Visible keys of this lane's row (bit 16*kt + v), all of them on a FULL tile.
+      uint32_t vis = 0xffffffffu;
+      float mx = neg_inf();
+      if (cls == TILE_MIXED) {
+        const int64_t key0 = t * kKeys;
+        int64_t lim64 = a.n - key0;
+        if (a.causal) lim64 = min(lim64, past + tok[rg] + 1 - key0);
+        const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
+        const uint8_t* mt = mrow[rg] ? mrow[rg] + key0 : nullptr;
+        vis = 0;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = 32 * kt + acc_key(v, hi);
+            bool ok = key < lim;
+            if (mt && ok) ok = mt[key] != 0;
+            vis |= ok ? (1u << (16 * kt + v)) : 0u;
+          }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, (vis >> (16 * kt + v)) & 1u ? s[rg][kt][v] : neg_inf());
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[rg][kt][v]);
+      }
+
+      // Running maximum, moved only when the tile's maximum exceeds it by
+      // more than 2^kLazy: p = exp2(s*c - m) then stays below 2^kLazy (exact
+      // in fp16/bf16 range) and the accumulators are rescaled rarely.
+      mx = pair_max(mx);
+      const float tmax = mx == neg_inf() ? neg_inf() : mx * a.c;
+      const bool move = tmax > m[rg] + kLazy;
+      const float mn = move ? tmax : m[rg];
+      const float alpha = move ? __builtin_amdgcn_exp2f(m[rg] - mn) : 1.f;
+      m[rg] = mn;
+      const float ms = (mn == neg_inf()) ? 0.f : mn;
+      if (__builtin_amdgcn_ballot_w64(move)) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[rg][dt][v] *= alpha;
+        l[rg] *= alpha;
+      }
+
+      // P^T operand of half kt, chunk c2: accumulators 8*c2 .. 8*c2+7 are keys
+      // 16*c2 + {4hi..4hi+3, 8+4hi..8+4hi+3} of the half, the order in which
+      // V^T is read. The row sum takes the rounded P, as the MFMA does.
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = 32 * kt + acc_key(v, hi);
-          bool ok = key < lim;
-          if (mt && ok) ok = mt[key] != 0;
-          vis |= ok ? (1u << (16 * kt + v)) : 0u;
+        for (int c2 = 0; c2 < 2; ++c2) {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int v0 = 8 * c2 + 2 * j;
+            float p0 = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v0], a.c, -ms));
+            float p1 = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v0 + 1], a.c, -ms));
+            if (cls == TILE_MIXED) {
+              p0 = (vis >> (16 * kt + v0)) & 1u ? p0 : 0.f;
+              p1 = (vis >> (16 * kt + v0 + 1)) & 1u ? p1 : 0.f;
+            }
+            w[j] = pack2<DT>(p0, p1);
+            l[rg] = Elem<DT>::dot2(w[j], kOnes<DT>, l[rg]);
+          }
+          pb[rg][kt][c2] = make_uint4(w[0], w[1], w[2], w[3]);
         }
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, (vis >> (16 * kt + v)) & 1u ? s[kt][v] : neg_inf());
-    } else {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
     }
 
-    // Running maximum, moved only when the tile's maximum exceeds it by more
-    // than 2^kLazy: p = exp2(s*c - m) then stays below 2^kLazy (exact in
-    // fp16/bf16 range) and the accumulators are rescaled rarely.
-    mx = pair_max(mx);
-    const float tmax = mx == neg_inf() ? neg_inf() : mx * a.c;
-    const bool move = tmax > m + kLazy;
-    const float mn = move ? tmax : m;
-    const float alpha = move ? __builtin_amdgcn_exp2f(m - mn) : 1.f;
-    m = mn;
-    const float ms = (m == neg_inf()) ? 0.f : m;
-    if (__builtin_amdgcn_ballot_w64(move)) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[dt][v] *= alpha;
-      l *= alpha;
-    }
-
-    // P^T operand of half kt, chunk c2: accumulators 8*c2 .. 8*c2+7 are keys
-    // 16*c2 + {4hi..4hi+3, 8+4hi..8+4hi+3} of the half, the order in which V^T
-    // is read. The row sum takes the rounded P, as the MFMA does.
+    // O^T += V^T . P^T: each V^T fragment read from LDS feeds kGroups MFMAs.
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int v0 = 8 * c2 + 2 * j;
-          float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][v0], a.c, -ms));
-          float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][v0 + 1], a.c, -ms));
-          if (cls == TILE_MIXED) {
-            p0 = (vis >> (16 * kt + v0)) & 1u ? p0 : 0.f;
-            p1 = (vis >> (16 * kt + v0 + 1)) & 1u ? p1 : 0.f;
-          }
-          w[j] = pack2<DT>(p0, p1);
-          l = Elem<DT>::dot2(w[j], kOnes<DT>, l);
-        }
-        const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+      for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           const uint16_t* vp = lv + (32 * dt + r32) * kVStride + 32 * kt + 16 * c2 + 4 * hi;
           const uint2 lo = *reinterpret_cast<const uint2*>(vp);
           const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
-          o[dt] = Mfma<DT>::mma(make_uint4(lo.x, lo.y, up.x, up.y), pb, o[dt]);
+          const uint4 va = make_uint4(lo.x, lo.y, up.x, up.y);
+#pragma unroll
+          for (int rg = 0; rg < kGroups; ++rg) o[rg][dt] = Mfma<DT>::mma(va, pb[rg][kt][c2], o[rg][dt]);
         }
-      }
 
     if (more) store_stage(st, s_k[buf ^ 1], s_v[buf ^ 1]);
     __syncthreads();
@@ -379,32 +409,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     t = tn;
   }
 
-  // Normalize and write this lane's 64 outputs: dims 32*dt + 8*j + 4*hi + 0..3.
-  const float lt = pair_sum(l);
-  if (!row_ok) return;
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (a.splits == 1) {
-    uint16_t* op = a.out + b * a.so_b + tok * a.so_t + hq * a.so_h + 4 * hi;
+  // Normalize and write the lane's outputs: dims 32*dt + 8*j + 4*hi + 0..3 of each row.
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+  for (int rg = 0; rg < kGroups; ++rg) {
+    const float lt = pair_sum(l[rg]);
+    if (!row_ok[rg]) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (a.splits == 1) {
+      uint16_t* op = a.out + b * a.so_b + tok[rg] * a.so_t + hq[rg] * a.so_h + 4 * hi;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t w0 = pack2<DT>(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv);
-        const uint32_t w1 = pack2<DT>(o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
-        *reinterpret_cast<uint2*>(op + 32 * dt + 8 * j) = make_uint2(w0, w1);
-      }
-    return;
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w0 = pack2<DT>(o[rg][dt][4 * j] * inv, o[rg][dt][4 * j + 1] * inv);
+          const uint32_t w1 = pack2<DT>(o[rg][dt][4 * j + 2] * inv, o[rg][dt][4 * j + 3] * inv);
+          *reinterpret_cast<uint2*>(op + 32 * dt + 8 * j) = make_uint2(w0, w1);
+        }
+    } else {
+      // Partial of this key split, merged by prefill_combine_kernel.
+      const int64_t prow =
+          ((static_cast<int64_t>(b) * a.splits + split) * a.q_len + tok[rg]) * (a.kv_heads * G) + hq[rg];
+      float* op = a.o_part + prow * kHeadDim + 4 * hi;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<float4*>(op + 32 * dt + 8 * j) = make_float4(
+              o[rg][dt][4 * j] * inv, o[rg][dt][4 * j + 1] * inv, o[rg][dt][4 * j + 2] * inv,
+              o[rg][dt][4 * j + 3] * inv);
+      if (hi == 0) a.lse_part[prow] = lt > 0.f ? m[rg] + __log2f(lt) : neg_inf();
+    }
   }
-  // Partial of this key split, merged by prefill_combine_kernel.
-  const int64_t prow = ((static_cast<int64_t>(b) * a.splits + split) * a.q_len + tok) * (a.kv_heads * G) + hq;
-  float* op = a.o_part + prow * kHeadDim + 4 * hi;
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<float4*>(op + 32 * dt + 8 * j) =
-          make_float4(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
-  if (hi == 0) a.lse_part[prow] = lt > 0.f ? m + __log2f(lt) : neg_inf();
 }
 
 // out[b, tok, hq, :] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the key
@@ -536,7 +571,8 @@ int plan_splits(int batch, int64_t q_len, int64_t n, int group, int kv_heads, in
     int cus = 0;
     const int rc = current_device_cus(&cus);
     if (rc != TC_OK) return rc;
-    const int64_t wgs = nblk * kv_heads * batch, slots = 2 * static_cast<int64_t>(cus);
+    // Work-groups resident per CU: one per wave slot of a SIMD (4 waves each).
+    const int64_t wgs = nblk * kv_heads * batch, slots = TC_PREFILL_WAVES * static_cast<int64_t>(cus);
     if (wgs < slots) s = (slots + wgs - 1) / wgs;
     s = std::min<int64_t>(s, std::max<int64_t>(1, ntiles / kMinSplitTiles));
   }
