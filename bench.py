@@ -300,7 +300,7 @@ def prefill_flops(q_len, n, causal_like, hq=HQ, d=D):
     return 4 * pairs * d * hq
 
 
-def measure_prefill(dev, steps):
+def measure_prefill(dev, steps, only_case=None):
     """Prefill attention at the Qwen3-4B shape (32 q / 8 kv heads, D=128, fp16): the
     GQA-native kernel vs the reference's GPU route (repeat_kv + SDPA with the same mask)."""
     import torch
@@ -322,11 +322,16 @@ def measure_prefill(dev, steps):
     cases = [("chunk_2048_on_7716", workloads.PREFILL_CHUNK, workloads.PREFILL_PAST + workloads.PREFILL_CHUNK, True),
              ("chunk_300_on_9700", 300, 10000, True),
              ("prompt_2048_causal", 2048, 2048, False)]
+    if only_case is not None:
+        # One workload alone (for counter runs); "nomask_2048_on_9764" is the chunk shape without a mask.
+        cases = [c for c in cases + [("nomask_2048_on_9764", 2048, 9764, None)] if c[0] == only_case]
+        if not cases:
+            raise SystemExit(f"unknown prefill case {only_case}")
     out = {}
     for name, L, n, masked in cases:
         q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, device=dev)
         mask = workloads.causal_mask(L, n, device=dev) if masked else None
-        causal = not masked
+        causal = masked is False
         scale = D ** -0.5
         iters = max(5, steps // 10)
         prefill.prefill_attention(q, k, v, mask, scale, causal)  # builds the mask's tile map once
@@ -334,8 +339,9 @@ def measure_prefill(dev, steps):
         ref = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
             q, attention.repeat_kv(k, HQ // HKV), attention.repeat_kv(v, HQ // HKV), attn_mask=mask, scale=scale,
             is_causal=causal).transpose(1, 2).contiguous(), iters)
-        tflops = prefill_flops(L, n, True) / (us * 1e-6) / 1e12
-        r = {"q_len": L, "kv_tokens": n, "mask": "bool [1,1,q,n] causal" if masked else "is_causal",
+        tflops = prefill_flops(L, n, masked is not None) / (us * 1e-6) / 1e12
+        r = {"q_len": L, "kv_tokens": n,
+             "mask": {True: "bool [1,1,q,n] causal", False: "is_causal", None: "none"}[masked],
              "splits": prefill.num_splits(1, L, n, HQ, HKV), "us_per_call": round(us, 1),
              "tflops": round(tflops, 1), "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16, 4),
              "reference_route_us": round(ref, 1), "speedup": round(ref / us, 2)}
@@ -454,6 +460,9 @@ def main():
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
+    ap.add_argument("--prefill-case", default=None,
+                    help="with --only prefill: one workload (chunk_2048_on_7716, chunk_300_on_9700, "
+                         "prompt_2048_causal, nomask_2048_on_9764)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -474,7 +483,7 @@ def main():
         print(json.dumps(bench_splice(dev, args.steps, args.warmup)))
         return
     if args.only == "prefill":
-        print(json.dumps(measure_prefill(dev, args.steps)))
+        print(json.dumps(measure_prefill(dev, args.steps, args.prefill_case)))
         return
     if args.only == "decode-step":
         print(json.dumps(measure_decode_step(dev, args.n)))
