@@ -47,8 +47,13 @@ constexpr int kRows = 4 * 32 * kGroups;  // query rows per work-group (4 waves)
 constexpr int kKeys = 64;          // keys per tile
 constexpr int kKStride = 136;      // halfs per K row in LDS (256 B + 16 B pad)
 constexpr int kVStride = 68;       // halfs per V^T row in LDS (128 B + 8 B pad)
+// V^T row of dim d: d + 2*(d / 32). With the 68-half stride this keeps the
+// 8-byte V^T reads (32 consecutive dims) and the transposing 8-byte stores
+// (8 dims apart) free of LDS bank conflicts.
+constexpr int kVRows = kHeadDim + 2 * (kHeadDim / 32 - 1);
+__host__ __device__ constexpr int vt_row(int d) { return d + 2 * (d >> 5); }
 constexpr int kKTile = kKeys * kKStride;
-constexpr int kVTile = kHeadDim * kVStride;
+constexpr int kVTile = kVRows * kVStride;
 
 enum : int { TILE_SKIP = 0, TILE_FULL = 1, TILE_MIXED = 2 };
 
@@ -165,7 +170,7 @@ __device__ __forceinline__ void store_stage(const Stage& s, uint16_t* lk, uint16
     const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
     const uint32_t x01 = __builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel);
     const uint32_t x23 = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);
-    *reinterpret_cast<uint2*>(lv + (8 * dc + e) * kVStride + 4 * kq) = make_uint2(x01, x23);
+    *reinterpret_cast<uint2*>(lv + vt_row(8 * dc + e) * kVStride + 4 * kq) = make_uint2(x01, x23);
   }
 }
 
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const uint16_t* vp = lv + (32 * dt + r32) * kVStride + 32 * kt + 16 * c2 + 4 * hi;
+          const uint16_t* vp = lv + vt_row(32 * dt + r32) * kVStride + 32 * kt + 16 * c2 + 4 * hi;
           const uint2 lo = *reinterpret_cast<const uint2*>(vp);
           const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
           const uint4 va = make_uint4(lo.x, lo.y, up.x, up.y);
