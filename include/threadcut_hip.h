@@ -260,7 +260,9 @@ size_t tc_prefill_workspace_bytes(int batch, int64_t q_len, int q_heads, int num
 size_t tc_prefill_tiles_bytes(int64_t q_len, int64_t n_tokens, int mask_batch, int q_heads, int kv_heads);
 
 /* Classifies every (query block of 128/g tokens, 64-key tile) of a boolean
- * mask as skip / full / mixed into `tiles` for tc_prefill_attention. One
+ * mask as skip / full / causal (exactly key <= n_tokens - q_len + token, the
+ * mask of a chunk on top of a cache) / mixed into `tiles` for
+ * tc_prefill_attention. One
  * read of the mask; the map stays valid while the mask is unchanged, so the
  * layers of one forward pass share it. Part of the prefill branch above
  * (threadcut/attention.py:43-46); the reference has no separate step. */

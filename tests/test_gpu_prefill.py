@@ -101,6 +101,20 @@ def test_key_splits(gpu, splits):
     assert torch.all(out[0, :3] == 0)
 
 
+@pytest.mark.parametrize("splits", [2, 5])
+def test_key_splits_with_batches(gpu, splits):
+    """Key splits and the combine index batches correctly (per-batch mask, bf16 too)."""
+    b, L, n = 3, 50, 700
+    q, k, v = workloads.prefill_inputs(50 + splits, batch=b, q_len=L, n=n, device=gpu)
+    g = torch.Generator().manual_seed(splits)
+    m = torch.rand((b, 1, L, n), generator=g) < 0.4
+    m[..., -1] = True
+    check(q, k, v, mask=m.to(gpu), splits=splits, label="split batch mask")
+    check(q, k, v, causal=False, splits=splits, label="split batch full")
+    qb, kb, vb = (t.to(torch.bfloat16) for t in (q, k, v))
+    check(qb, kb, vb, mask=workloads.causal_mask(L, n, batch=b).to(gpu), splits=splits, label="split batch bf16")
+
+
 def test_short_chunk_on_long_cache_uses_splits(gpu):
     """A few hundred new tokens on top of a 10k cache: too few query blocks to fill
     the GPU, so the keys are split."""
@@ -108,6 +122,49 @@ def test_short_chunk_on_long_cache_uses_splits(gpu):
     assert prefill.num_splits(1, 2048, 9764, 32, 8) == 1
     q, k, v = workloads.prefill_inputs(40, q_len=300, n=10000, device=gpu)
     check(q, k, v, mask=workloads.causal_mask(300, 10000).to(gpu), label="short chunk")
+
+
+def classify_tiles(mask, q_heads, kv_heads):
+    """The tile map by its definition, in numpy: per (mask batch, query block of 128/g
+    tokens, 64-key tile): 0 no visible key, 1 all visible, 3 exactly the end-aligned
+    causal rule, 2 otherwise."""
+    m = mask[:, 0].cpu().numpy()
+    mb, L, n = m.shape
+    tokens = 128 // (q_heads // kv_heads)
+    nblk, nt = -(-L // tokens), -(-n // 64)
+    out = np.zeros((mb, nblk, nt), np.uint8)
+    past = n - L
+    for b in range(mb):
+        for i in range(nblk):
+            t0, t1 = i * tokens, min(L, (i + 1) * tokens)
+            for j in range(nt):
+                blk = np.zeros((t1 - t0, 64), bool)
+                blk[:, :min(64, n - 64 * j)] = m[b, t0:t1, 64 * j:64 * j + 64]
+                keys = 64 * j + np.arange(64)
+                causal = (keys[None, :] <= past + np.arange(t0, t1)[:, None]) & (keys[None, :] < n)
+                out[b, i, j] = 0 if not blk.any() else 1 if blk.all() else 3 if (blk == causal).all() else 2
+    return out
+
+
+def test_mask_tile_map(gpu):
+    """The one-pass tile map equals the classification by definition (sdpa_mask's chunk
+    mask, one flipped element, random masks per batch)."""
+    cases = [workloads.causal_mask(200, 1000), workloads.causal_mask(37, 130, batch=2).clone()]
+    cases[1][1, 0, 5, 3] = False  # batch 1 leaves the causal rule in one tile
+    g = torch.Generator().manual_seed(3)
+    cases.append(torch.rand((2, 1, 90, 300), generator=g) < 0.5)
+    for m in cases:
+        for hq, hkv in ((32, 8), (8, 8)):
+            md = m.to(gpu)
+            prefill._tile_cache = None
+            tiles = prefill.mask_tiles(md, hq, hkv)
+            torch.cuda.synchronize()
+            want = classify_tiles(md if md.stride(0) else md[:1], hq, hkv)
+            mb, nblk, nt = want.shape
+            pitch = -(-nt // 8) * 8  # rows padded to 8 tiles, the padding SKIP (0)
+            got = tiles.cpu().numpy()[:mb * nblk * pitch].reshape(mb, nblk, pitch)
+            assert np.array_equal(got[..., :nt], want) and not got[..., nt:].any()
+    assert 3 in classify_tiles(cases[0], 32, 8) and 2 in classify_tiles(cases[1], 32, 8)
 
 
 def test_rows_without_visible_keys_are_zero(gpu):

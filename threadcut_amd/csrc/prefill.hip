@@ -18,14 +18,17 @@
 //                   never moves between lanes.
 // The online softmax runs per query row in fp32, log2 domain, as
 // p = exp2(s * c - m) with c = |scale| * log2(e) (a negative scale flips the
-// sign bits of Q instead). The accumulators are rescaled only when some
-// row's maximum moved.
+// sign bits of Q instead). The running maximum m moves only when a tile's
+// maximum exceeds it by more than 2^8, so the accumulators are rescaled
+// rarely.
 //
 // Every tile is classified for the whole work-group: SKIP (no row sees any
 // of its keys: not loaded), FULL (every row sees every key: no per-element
-// test) or MIXED (per-element test). Without a mask the class follows from
-// n and the causal diagonal; with a boolean mask it is read from a map that
-// tc_prefill_mask_tiles builds in one pass over the mask, once per mask.
+// test), CAUSAL (per-element test by the end-aligned causal rule) or MIXED
+// (per-element test against the mask bytes). Without a mask the class
+// follows from n and the causal diagonal; with a boolean mask it is read
+// from a map that tc_prefill_mask_tiles builds in one pass over the mask,
+// once per mask.
 // Tiles are double-buffered: the next active tile's global loads are in
 // flight while the current one is multiplied.
 #include <algorithm>
@@ -55,7 +58,9 @@ __host__ __device__ constexpr int vt_row(int d) { return d + 2 * (d >> 5); }
 constexpr int kKTile = kKeys * kKStride;
 constexpr int kVTile = kVRows * kVStride;
 
-enum : int { TILE_SKIP = 0, TILE_FULL = 1, TILE_MIXED = 2 };
+// TILE_CAUSAL: the tile's mask is exactly the end-aligned causal rule
+// (key <= n - q_len + token), so its elements are tested arithmetically.
+enum : int { TILE_SKIP = 0, TILE_FULL = 1, TILE_MIXED = 2, TILE_CAUSAL = 3 };
 
 // Waves per SIMD the register allocation targets: 2 leaves 256 registers a
 // lane and matches the two 68 KB work-groups the LDS of a CU holds.
@@ -73,7 +78,7 @@ struct PrefillArgs {
   const uint16_t* k;
   const uint16_t* v;
   const uint8_t* mask;      // null, or [mb, L, n] booleans, keys contiguous (batch stride 0 broadcasts)
-  const uint8_t* tiles;     // null, or the tile classes of `mask` [mb][nblk][ntiles]
+  const uint8_t* tiles;     // null, or the tile classes of `mask` [mb][nblk][pitch]
   uint16_t* out;            // [b, L, hq, d]
   int64_t sq_b, sq_h, sq_t;
   int64_t sk_b, sk_h, sk_t;
@@ -82,6 +87,7 @@ struct PrefillArgs {
   int64_t so_b, so_t, so_h;
   int64_t q_len, n;         // query tokens, keys (the queries sit at positions n - q_len ..)
   int64_t nblk, ntiles;     // query blocks per (batch, KV head); 64-key tiles of n
+  int64_t pitch;            // tile map row length: ntiles rounded up to 8 (padding reads as SKIP)
   int64_t split_tiles;      // tiles per key split
   float* o_part;            // splits > 1: [b, splits, L, hq, d] fp32, normalized per split
   float* lse_part;          // splits > 1: [b, splits, L, hq] log2-sum-exp of the split (-inf if empty)
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
   const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
   const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
-  const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.ntiles : nullptr;
+  const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.pitch : nullptr;
 
   // Tiles this work-group may need: its split's share of all n keys, cut at
   // its last query's position when causal.
@@ -266,9 +272,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     if (a.causal && key0 + kKeys - 1 > past + tok0) return TILE_MIXED;
     return TILE_FULL;
   };
+  // First active tile at or after t (nt if none). With a map, eight classes
+  // are tested per 8-byte read (rows are 8-aligned and padded with SKIP).
   auto next_active = [&](int64_t t) -> int64_t {
-    while (t < nt && tile_class(t) == TILE_SKIP) ++t;
-    return t;
+    if (!tcls) {
+      while (t < nt && tile_class(t) == TILE_SKIP) ++t;
+      return t;
+    }
+    while (t < nt) {
+      const uint64_t w = *reinterpret_cast<const uint64_t*>(tcls + (t & ~int64_t(7))) >> (8 * (t & 7));
+      if (w) return min(nt, t + (__builtin_ctzll(w) >> 3));
+      t = (t & ~int64_t(7)) + 8;
+    }
+    return nt;
   };
 
   float m[kGroups], l[kGroups];
@@ -283,20 +299,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int v = 0; v < 16; ++v) o[rg][dt][v] = 0.f;
   }
 
+  // Active tiles t (in LDS), tn (loading) and the class of each, found one
+  // iteration ahead so the tile map's reads are off the critical path.
   Stage st;
   int64_t t = next_active(t_begin);
+  int cls_t = t < nt ? tile_class(t) : TILE_SKIP;
   if (t < nt) {
     load_stage(st, kslab, vslab, row_k, row_v, t * kKeys, a.n);
     store_stage(st, s_k[0], s_v[0]);
   }
+  int64_t tn = t < nt ? next_active(t + 1) : nt;
+  int cls_n = tn < nt ? tile_class(tn) : TILE_SKIP;
   __syncthreads();
 
   int buf = 0;
   while (t < nt) {
-    const int64_t tn = next_active(t + 1);
     const bool more = tn < nt;
     if (more) load_stage(st, kslab, vslab, row_k, row_v, tn * kKeys, a.n);
-    const int cls = tile_class(t);
+    const int64_t tnn = more ? next_active(tn + 1) : nt;
+    const int cls_nn = tnn < nt ? tile_class(tnn) : TILE_SKIP;
+    const int cls = cls_t;
     const uint16_t* lk = s_k[buf];
     const uint16_t* lv = s_v[buf];
 
@@ -324,12 +346,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       // Visible keys of this lane's row (bit 16*kt + v), all of them on a FULL tile.
       uint32_t vis = 0xffffffffu;
       float mx = neg_inf();
-      if (cls == TILE_MIXED) {
+      if (cls != TILE_FULL) {
         const int64_t key0 = t * kKeys;
         int64_t lim64 = a.n - key0;
-        if (a.causal) lim64 = min(lim64, past + tok[rg] + 1 - key0);
+        if (a.causal || cls == TILE_CAUSAL) lim64 = min(lim64, past + tok[rg] + 1 - key0);
         const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
-        const uint8_t* mt = mrow[rg] ? mrow[rg] + key0 : nullptr;
+        const uint8_t* mt = (cls == TILE_MIXED && mrow[rg]) ? mrow[rg] + key0 : nullptr;
         vis = 0;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -382,7 +404,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
             const int v0 = 8 * c2 + 2 * j;
             float p0 = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v0], a.c, -ms));
             float p1 = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v0 + 1], a.c, -ms));
-            if (cls == TILE_MIXED) {
+            if (cls != TILE_FULL) {
               p0 = (vis >> (16 * kt + v0)) & 1u ? p0 : 0.f;
               p1 = (vis >> (16 * kt + v0 + 1)) & 1u ? p1 : 0.f;
             }
@@ -412,6 +434,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     __syncthreads();
     buf ^= 1;
     t = tn;
+    cls_t = cls_n;
+    tn = tnn;
+    cls_n = cls_nn;
   }
 
   // Normalize and write the lane's outputs: dims 32*dt + 8*j + 4*hi + 0..3 of each row.
@@ -484,26 +509,33 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* o_par
 // One wave per (64-key tile, query block, mask batch): lane = key in the tile.
 __global__ __launch_bounds__(64) void mask_tiles_kernel(const uint8_t* mask, int64_t sm_b, int64_t sm_q,
                                                        int64_t sm_k, int64_t q_len, int64_t n, int tokens,
-                                                       int64_t nblk, int64_t ntiles, uint8_t* tiles) {
+                                                       int64_t nblk, int64_t pitch, uint8_t* tiles) {
   const int lane = threadIdx.x;
   const int64_t t = blockIdx.x, blk = blockIdx.y, bm = blockIdx.z;
   const int64_t key = t * kKeys + lane;
   const int64_t tok0 = blk * tokens;
   const int64_t tok_end = min(tok0 + tokens, q_len);
-  bool any = false, all = key < n;
+  const int64_t past = n - q_len;
+  bool any = false, all = key < n, causal = true;
   if (key < n) {
     const uint8_t* p = mask + bm * sm_b + key * sm_k;
     for (int64_t tok = tok0; tok < tok_end; ++tok) {
       const bool x = p[tok * sm_q] != 0;
       any |= x;
       all &= x;
+      causal &= x == (key <= past + tok);
     }
   }
   const uint64_t any_w = __builtin_amdgcn_ballot_w64(any);
   const uint64_t all_w = __builtin_amdgcn_ballot_w64(all);
-  if (lane == 0)
-    tiles[(bm * nblk + blk) * ntiles + t] =
-        static_cast<uint8_t>(any_w == 0 ? TILE_SKIP : (all_w == ~uint64_t(0) ? TILE_FULL : TILE_MIXED));
+  const uint64_t causal_w = __builtin_amdgcn_ballot_w64(causal);
+  if (lane == 0) {
+    const int cls = any_w == 0                  ? TILE_SKIP
+                    : all_w == ~uint64_t(0)     ? TILE_FULL
+                    : causal_w == ~uint64_t(0)  ? TILE_CAUSAL
+                                                : TILE_MIXED;
+    tiles[(bm * nblk + blk) * pitch + t] = static_cast<uint8_t>(cls);
+  }
 }
 
 template <int DT>
@@ -552,6 +584,8 @@ int check_mask_strides(const int64_t* st) {
 }
 
 // Tile map geometry: query blocks of 128/g tokens, 64-key tiles.
+int64_t map_pitch(int64_t ntiles) { return (ntiles + 7) & ~int64_t(7); }
+
 void tile_geometry(int64_t q_len, int64_t n, int group, int64_t* nblk, int64_t* ntiles) {
   const int64_t tokens = kRows / group;
   *nblk = (q_len + tokens - 1) / tokens;
@@ -620,7 +654,7 @@ extern "C" size_t tc_prefill_tiles_bytes(int64_t q_len, int64_t n_tokens, int ma
   if (q_len < 0 || n_tokens < q_len || mask_batch < 1 || check_group(q_heads, kv_heads, &group) != TC_OK) return 0;
   int64_t nblk, ntiles;
   tile_geometry(q_len, n_tokens, group, &nblk, &ntiles);
-  return static_cast<size_t>(mask_batch * nblk * ntiles);
+  return static_cast<size_t>(mask_batch * nblk * map_pitch(ntiles));
 }
 
 extern "C" int tc_prefill_mask_tiles(const uint8_t* mask_dev, const int64_t mask_strides[3], int mask_batch,
@@ -638,7 +672,8 @@ extern "C" int tc_prefill_mask_tiles(const uint8_t* mask_dev, const int64_t mask
     return fail(TC_ERR_INVALID_ARGUMENT, "mask_batch %d with a broadcast (stride 0) mask batch", mask_batch);
   int64_t nblk, ntiles;
   tile_geometry(q_len, n_tokens, group, &nblk, &ntiles);
-  const size_t need = static_cast<size_t>(mask_batch * nblk * ntiles);
+  const int64_t pitch = map_pitch(ntiles);
+  const size_t need = static_cast<size_t>(mask_batch * nblk * pitch);
   if (need == 0) return TC_OK;
   if (!mask_dev || !tiles_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null mask or tile map pointer");
   if (tiles_bytes < need)
@@ -646,9 +681,11 @@ extern "C" int tc_prefill_mask_tiles(const uint8_t* mask_dev, const int64_t mask
   if (ntiles > 0x7fffffff || nblk > 65535)
     return fail(TC_ERR_UNSUPPORTED, "mask of %lld x %lld exceeds the tile grid", (long long)q_len,
                 (long long)n_tokens);
-  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(nblk), static_cast<unsigned>(mask_batch));
+  if (reinterpret_cast<uintptr_t>(tiles_dev) & 7u) return fail(TC_ERR_ALIGNMENT, "tile map must be 8-byte aligned");
+  // The padding tiles (keys past n) classify as SKIP, so whole rows are written.
+  const dim3 grid(static_cast<unsigned>(pitch), static_cast<unsigned>(nblk), static_cast<unsigned>(mask_batch));
   hipLaunchKernelGGL(mask_tiles_kernel, grid, dim3(64), 0, static_cast<hipStream_t>(stream), mask_dev,
-                     mask_strides[0], mask_strides[1], mask_strides[2], q_len, n_tokens, kRows / group, nblk, ntiles,
+                     mask_strides[0], mask_strides[1], mask_strides[2], q_len, n_tokens, kRows / group, nblk, pitch,
                      tiles_dev);
   return hip_status(hipGetLastError(), "mask tile launch");
 }
@@ -691,7 +728,9 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
     if (causal) return fail(TC_ERR_INVALID_ARGUMENT, "pass either a mask or causal, not both");
     if ((rc = check_mask_strides(mask_strides)) != TC_OK) return rc;
     if (mask_tiles_dev) {
-      const size_t need = static_cast<size_t>((mask_strides[0] ? batch : 1) * nblk * ntiles);
+      const size_t need = static_cast<size_t>((mask_strides[0] ? batch : 1) * nblk * map_pitch(ntiles));
+      if (reinterpret_cast<uintptr_t>(mask_tiles_dev) & 7u)
+        return fail(TC_ERR_ALIGNMENT, "tile map must be 8-byte aligned");
       if (mask_tiles_bytes < need)
         return fail(TC_ERR_WORKSPACE, "tile map holds %zu bytes, this call reads %zu", mask_tiles_bytes, need);
     }
@@ -731,6 +770,7 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
   a.n = n_tokens;
   a.nblk = nblk;
   a.ntiles = ntiles;
+  a.pitch = map_pitch(ntiles);
   a.kv_heads = kv_heads;
   a.causal = causal ? 1 : 0;
   a.neg = scale < 0.f ? 1 : 0;
