@@ -54,6 +54,7 @@ namespace {
 #endif
 
 constexpr int kHeadDim = 128;
+constexpr int64_t kMaxTokens = int64_t(1) << 29;  // token positions stay 32-bit in the kernel
 constexpr int kWaves = TC_DECODE_WAVES;
 constexpr int kDepth = TC_DECODE_DEPTH;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
@@ -244,12 +245,14 @@ struct Tile {
   uint4 v[4];  // register j: token slot j
 };
 
-__device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char* vslab, int64_t row_k,
-                                          int64_t row_v, int64_t t0, int64_t end, const int32_t* koff,
+__device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char* vslab, int32_t row_k,
+                                          int32_t row_v, int32_t t0, int32_t end, const int32_t* koff,
                                           const int32_t* voff) {
-  const int64_t rows = min(max(end - t0, int64_t(0)), int64_t(16));
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kslab + t0 * row_k, static_cast<int32_t>(rows * row_k));
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vslab + t0 * row_v, static_cast<int32_t>(rows * row_v));
+  // The clamp is wave-uniform, but i32 min/max select v_med3 (a VGPR);
+  // readfirstlane keeps the buffer resource in SGPRs (no waterfall loop).
+  const int32_t rows = __builtin_amdgcn_readfirstlane(min(max(end - t0, 0), 16));
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kslab + static_cast<int64_t>(t0) * row_k, rows * row_k);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vslab + static_cast<int64_t>(t0) * row_v, rows * row_v);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     t.k[j] = bload16(rk, koff[j]);
@@ -349,26 +352,48 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   // into [0, n]. With an append the new token is one more, read from
   // k_new/v_new and written to row `len`, so len stays below n: n - 1
   // without lengths, lens[b] (the append position) clamped to n - 1 with.
-  const int64_t len_cap = a.k_new ? a.n - 1 : a.n;
-  const int64_t len = a.lens ? min(max(static_cast<int64_t>(a.lens[b]), int64_t(0)), len_cap) : len_cap;
-  // The wave's 16-token tiles: first, first + stride, ... with tokens < end.
-  // Contiguous: split s, wave w own [s*T + w*T/W, s*T + (w+1)*T/W). Interleaved:
-  // all S*W waves of a head sweep the cache together, wave g taking tiles
-  // g, g + S*W, ..., so the loads in flight at any moment are adjacent in HBM.
-  int64_t first_tile, tile_stride, end;
+  // Token positions are 32-bit (the host keeps n and S * T below 2^30), and
+  // nothing before the first K/V requests divides: every wave runs this
+  // prologue before its first load, so its length is latency.
+  const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
+  const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
+  const int32_t row_k = static_cast<int32_t>(a.sk_t) * 2, row_v = static_cast<int32_t>(a.sv_t) * 2;
+  // Materialise the slab addresses here so their kernel arguments are fetched
+  // with the others at entry (one scalar round trip instead of two).
+  __asm__ volatile("" ::"s"(kslab), "s"(vslab));
+  const int32_t n = static_cast<int32_t>(a.n);
+  const int32_t len_cap = a.k_new ? n - 1 : n;
+  int32_t len = len_cap;
+  if (a.lens) len = min(max(a.lens[b], 0), len_cap);
+  // The wave's 16-token tiles start at tok and advance by tok_step while
+  // below end. Contiguous: split s, wave w own [s*T + w*T/W, s*T + (w+1)*T/W).
+  // Interleaved: all S*W waves of a head sweep the cache together, wave g
+  // taking tiles g, g + S*W, ..., so the loads in flight at any moment are
+  // adjacent in HBM.
+  int32_t tok, tok_step, end;
   if (a.interleave) {
-    first_tile = static_cast<int64_t>(split) * kWaves + wave;
-    tile_stride = static_cast<int64_t>(a.splits) * kWaves;
+    tok = (split * kWaves + wave) * kWaveIter;
+    tok_step = a.splits * kWaves * kWaveIter;
     end = len;
   } else {
-    const int wave_tokens = a.split_tokens / kWaves;
-    const int64_t start = static_cast<int64_t>(split) * a.split_tokens + static_cast<int64_t>(wave) * wave_tokens;
-    first_tile = start / kWaveIter;
-    tile_stride = 1;
-    end = min(start + wave_tokens, len);
+    const int32_t wave_tokens = a.split_tokens / kWaves;
+    tok = split * a.split_tokens + wave * wave_tokens;
+    tok_step = kWaveIter;
+    end = min(tok + wave_tokens, len);
   }
-  const int64_t first_tok = first_tile * kWaveIter;
-  const int64_t ntiles = end > first_tok ? ceil_div(end - first_tok, kWaveIter * tile_stride) : 0;
+
+  int32_t koff[4], voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    koff[j] = (4 * (j ^ (c >> 2)) + grp) * row_k + 16 * c;
+    voff[j] = (4 * j + grp) * row_v + 16 * c;
+  }
+  // Ring of kDepth tiles, the first kDepth - 1 requested before anything
+  // else. Loads past `end` read nothing (the buffer range is empty there).
+  Tile t[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth - 1; ++d)
+    load_tile(t[d], kslab, vslab, row_k, row_v, tok + d * tok_step, end, koff, voff);
 
   // The lane's 8 dims of every query row, in the lane's head order.
   uint32_t qw[GP][4];
@@ -378,45 +403,29 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
 #pragma unroll
     for (int hh = 0; hh < GP; ++hh) {
       const int row = hh ^ hp;
-      uint4 t = make_uint4(0u, 0u, 0u, 0u);
-      if (row < a.group) t = *reinterpret_cast<const uint4*>(qb + row * a.sq_g);
-      qw[hh][0] = t.x; qw[hh][1] = t.y; qw[hh][2] = t.z; qw[hh][3] = t.w;
+      uint4 q4 = make_uint4(0u, 0u, 0u, 0u);
+      if (row < a.group) q4 = *reinterpret_cast<const uint4*>(qb + row * a.sq_g);
+      qw[hh][0] = q4.x; qw[hh][1] = q4.y; qw[hh][2] = q4.z; qw[hh][3] = q4.w;
     }
-  }
-
-  const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
-  const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
-  const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
-  int32_t koff[4], voff[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    koff[j] = static_cast<int32_t>((4 * (j ^ (c >> 2)) + grp) * row_k + 16 * c);
-    voff[j] = static_cast<int32_t>((4 * j + grp) * row_v + 16 * c);
   }
 
   Stream<DT, GP> st;
   st.init();
   const int my_slot = 4 * (c >> 2) + grp;  // token slot of the lane's score(s)
 
-  if (ntiles > 0) {
-    // Ring of kDepth tiles: tile d of a round is computed while the next
-    // kDepth - 1 tiles are in flight (indices fold to constants when unrolled).
-    // Loads past `end` read nothing (the buffer range is empty there).
-    const int64_t tok_step = tile_stride * kWaveIter;
-    Tile t[kDepth];
-#pragma unroll
-    for (int d = 0; d < kDepth - 1; ++d)
-      load_tile(t[d], kslab, vslab, row_k, row_v, first_tok + d * tok_step, end, koff, voff);
-    for (int64_t i = 0;; i += kDepth) {
+  if (tok < end) {
+    // Tile d of a round is computed while the next kDepth - 1 tiles are in
+    // flight (ring indices fold to constants when unrolled).
+    for (;;) {
       bool done = false;
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
         if (!done) {
-          const int64_t tok = first_tok + (i + d) * tok_step;
           load_tile(t[(d + kDepth - 1) % kDepth], kslab, vslab, row_k, row_v, tok + (kDepth - 1) * tok_step, end,
                     koff, voff);
           st.step(t[d], qw, tok + my_slot < end, a.scale_log2);
-          done = i + d + 1 >= ntiles;
+          tok += tok_step;
+          done = tok >= end;
         }
       }
       if (done) break;
@@ -430,13 +439,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     const char* vn = reinterpret_cast<const char*>(a.v_new + b * a.svn_b + h * a.svn_h);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kn, kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vn, kHeadDim * 2);
-    Tile t;
+    Tile tn;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      t.k[j] = bload16(rk, koff[j]);
-      t.v[j] = bload16(rv, voff[j]);
+      tn.k[j] = bload16(rk, koff[j]);
+      tn.v[j] = bload16(rv, voff[j]);
     }
-    st.step(t, qw, my_slot == 0, a.scale_log2);
+    st.step(tn, qw, my_slot == 0, a.scale_log2);
     if (lane < 32) {
       const bool is_v = lane >= 16;
       const int chunk = 8 * (lane & 15);
@@ -498,9 +507,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       L += s_l[w][hh] * f;
       O += s_acc[w][hh][d] * f;
     }
-    a.o_part[(part * a.group + hh) * kHeadDim + d] = O / (L == 0.f ? 1.f : L);
+    // L >= 1 whenever a token was seen (the maximum contributes exp2(0)), so
+    // the hardware reciprocal and log2 need no denormal or zero handling.
+    a.o_part[(part * a.group + hh) * kHeadDim + d] = L == 0.f ? 0.f : O * __builtin_amdgcn_rcpf(L);
     if (d == 0)
-      a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (M + __log2f(L)) * kLn2;
+      a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (M + __builtin_amdgcn_logf(L)) * kLn2;
   }
 }
 
@@ -730,6 +741,8 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   if ((rc = check_strides("k", k_strides, 3)) != TC_OK) return rc;
   if ((rc = check_strides("v", v_strides, 3)) != TC_OK) return rc;
   if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
+  if (n_tokens > kMaxTokens)
+    return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld above %lld", (long long)n_tokens, (long long)kMaxTokens);
   if (split_tokens <= 0 || split_tokens % kSplitGranule != 0)
     return fail(TC_ERR_INVALID_ARGUMENT, "split_tokens %d must be a positive multiple of %d", split_tokens,
                 kSplitGranule);
@@ -738,6 +751,9 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   if (static_cast<int64_t>(num_splits) * split_tokens < n_tokens)
     return fail(TC_ERR_INVALID_ARGUMENT, "%d splits of %d tokens do not cover %lld tokens", num_splits, split_tokens,
                 (long long)n_tokens);
+  if (static_cast<int64_t>(num_splits) * split_tokens > 2 * kMaxTokens)
+    return fail(TC_ERR_INVALID_ARGUMENT, "%d splits of %d tokens span more than %lld tokens", num_splits,
+                split_tokens, (long long)(2 * kMaxTokens));
   if (num_splits == 0) return TC_OK;
   if (!isfinite(scale)) return fail(TC_ERR_INVALID_ARGUMENT, "scale is not finite");
   // Per-lane buffer offsets span 16 token rows in 32 bits.
