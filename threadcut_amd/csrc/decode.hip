@@ -1,26 +1,36 @@
 // Split-KV GQA flash-decode for gfx950: a partial online-softmax kernel over
-// (split, kv head, sequence) work-groups and a separate log-sum-exp combine.
+// (split, kv head, sequence) work-groups on the matrix cores, and a separate
+// log-sum-exp combine.
 //
 // Reference semantics: threadcut/flash_decode.py:21-54 (`_partial`: fp32
-// math, scale applied after q.k, -inf guards, out = acc / l, lse = m + log l)
-// and :57-69 (decode_attention: splits = cdiv(n, split), merge with
-// softmax(lse) weights, cast to q.dtype).
+// softmax, scale applied after q.k, -inf guards, out = acc / l,
+// lse = m + log l) and :57-69 (decode_attention: splits = cdiv(n, split),
+// merge with softmax(lse) weights, cast to q.dtype).
 //
-// Layout of one wave64 over the cache: a 16-token iteration issues four
-// 1 KiB-contiguous 128-bit loads of K (and four of V). Lane l reads token
-// t0 + 4j + (l >> 4), dims 8*(l & 15) .. +8, for j = 0..3, so the wave's 16
-// lanes of a row hold one token and the four rows hold four tokens. The g
-// query heads of the KV head stay in registers and share every K/V element.
-//   - q.k: v_dot2_f32_{f16,bf16} over the lane's 8 dims, then a DPP
-//     reduce-scatter inside each row (4 steps) leaves every lane with the full
-//     score of one (token, head) pair (two for g > 4);
-//   - online softmax per row and head in the log2 domain (exp2), max via two
-//     DPP steps over the four lanes of a head;
-//   - p.v: each lane accumulates its 8 dims for the row's token, p broadcast
-//     from the owning lane with DPP row_newbcast.
-// Four rows x four waves are independent online-softmax streams; they are
-// merged once at the end (cross-row shuffles, then LDS across waves) so each
+// Per wave and 16-token tile, with n = lane % 16 (query head: a column of
+// every 16x16 MFMA block; columns n >= G hold zeros) and g = lane / 16:
+//   S^T[token][head] = K[token][:] . Q[head][:]   four v_mfma_f32_16x16x32
+//     (k = 32 dims each). A = K rows: lane l loads token l % 16, bytes
+//     [64 i + 16 g, +16) of its row for block i, so each load instruction
+//     reads 16 rows x 64 contiguous bytes; B = Q with the same dims, held in
+//     registers for the whole kernel. Lane l receives S^T[4g + r][n], r < 4.
+//   softmax per head in fp32, log2 domain, the tile maximum across the four
+//     lane groups by two permlane swaps; the running maximum moves only when
+//     a tile's exceeds it by 2^8 (p is then at most 2^8), so the accumulators
+//     are rescaled rarely.
+//   O^T[dim][head] += V^T[dim][token] . P^T[token][head]   eight
+//     v_mfma_f32_16x16x16 (k = 16 tokens), each twice: with P rounded to the
+//     element type and with the rounding residue, so the weights carry about
+//     16 (bf16) or 22 (fp16) significant bits. P^T leaves the S^T registers as
+//     the B operand without moving between lanes (lane l holds tokens
+//     4g..4g+3 of head n in both layouts). V is loaded as 4 tokens x 8 dims
+//     per lane, transposed in registers (v_perm) and written to the wave's
+//     own LDS region as V^T rows, which the A operand reads back 8 bytes per
+//     lane.
+// The matrix core sums over a wave's tokens, so a wave's accumulator is
+// complete; the four waves of a work-group are merged through LDS and the
 // work-group writes one (o, lse) partial per query head.
+
 #include <math.h>
 
 #include <algorithm>
@@ -39,9 +49,6 @@ namespace {
 #endif
 #ifndef TC_DECODE_AUX
 #define TC_DECODE_AUX 2     // cache-policy bits of the K/V buffer loads (2: non-temporal stream)
-#endif
-#ifndef TC_DECODE_PERMLANE
-#define TC_DECODE_PERMLANE 1  // merge the four rows of a wave with v_permlane{16,32}_swap
 #endif
 #ifndef TC_DECODE_INTERLEAVE
 #define TC_DECODE_INTERLEAVE 1  // tc_decode_attention deals tiles round-robin over the splits
@@ -94,107 +101,7 @@ struct CombineArgs {
   int heads, group, splits;
 };
 
-__device__ __forceinline__ uint4 load16(const uint16_t* p) {
-  return *reinterpret_cast<const uint4*>(p);
-}
-
-__device__ __forceinline__ uint32_t word(const uint4& x, int i) {
-  return i == 0 ? x.x : (i == 1 ? x.y : (i == 2 ? x.z : x.w));
-}
-
-// Lane permutations that make the row reduction select-free.
-//
-// A lane's partial dots are x[slot' * GP + head'] (slot' < 4, head' < GP):
-// K register slot' holds token slot slot' ^ (c >> 2) of the iteration and q
-// register head' holds query row head' ^ head_perm(c). Written as a bit
-// vector, register r of lane c then carries value r ^ X(c), where X is the
-// linear map that sends the DPP partner patterns used below (c ^ 8, c ^ 7
-// via half-mirror, c ^ 2, c ^ 1) to the register bits halved at each step.
-// Every step is x[i] += dpp(x[i + K/2]) on all lanes: no per-lane selects.
-template <int GP>
-__device__ __forceinline__ int head_perm(int c) {
-  const int flip = ((c >> 2) & 1) ? 3 : 0;
-  if constexpr (GP == 1) return 0;
-  else if constexpr (GP == 2) return ((c >> 1) & 1) ^ ((c >> 2) & 1);
-  else if constexpr (GP == 4) return (c & 3) ^ flip;
-  else return 2 * ((c & 3) ^ flip);
-}
-
-// Row lane holding the score of (token slot j, head hh) after the scatter.
-template <int GP>
-constexpr int owner_lane(int j, int hh) {
-  return GP == 1 ? 4 * j
-       : GP == 2 ? 4 * j + 2 * (hh ^ (j & 1))
-       : GP == 4 ? 4 * j + (hh ^ ((j & 1) ? 3 : 0))
-                 : 4 * j + ((hh >> 1) ^ ((j & 1) ? 3 : 0));
-}
-
-// Register (index < VPL) of that lane holding it.
-template <int GP>
-constexpr int owner_reg(int hh) { return GP == 8 ? (hh & 1) : 0; }
-
-// Sum of the NV = 4 * GP partial dots over the 16 lanes of each row,
-// scattered: lane c keeps the totals of its first VPL registers.
-template <int NV>
-__device__ __forceinline__ void row_reduce_scatter(float* x) {
-#pragma unroll
-  for (int i = 0; i < NV / 2; ++i) x[i] += dpp<DPP_ROW_ROR8>(x[i + NV / 2]);
-#pragma unroll
-  for (int i = 0; i < NV / 4; ++i) x[i] += dpp<DPP_ROW_HALF_MIRROR>(x[i + NV / 4]);
-  if constexpr (NV / 8 >= 1) {
-#pragma unroll
-    for (int i = 0; i < NV / 8; ++i) x[i] += dpp<DPP_QUAD_XOR2>(x[i + NV / 8]);
-  } else {
-    x[0] += dpp<DPP_QUAD_XOR2>(x[0]);
-  }
-  if constexpr (NV / 16 >= 1) {
-#pragma unroll
-    for (int i = 0; i < NV / 16; ++i) x[i] += dpp<DPP_QUAD_XOR1>(x[i + NV / 16]);
-  } else {
-    x[0] += dpp<DPP_QUAD_XOR1>(x[0]);
-  }
-}
-
-// All-reduce over the four lanes of a row that own one head (c, c^8, c^7, c^15).
-__device__ __forceinline__ float head_max(float t) {
-  t = fmaxf(t, dpp<DPP_ROW_ROR8>(t));
-  return fmaxf(t, dpp<DPP_ROW_HALF_MIRROR>(t));
-}
-__device__ __forceinline__ float head_sum(float t) {
-  t += dpp<DPP_ROW_ROR8>(t);
-  return t + dpp<DPP_ROW_HALF_MIRROR>(t);
-}
-
-// Value of x held by lane k of the caller's row; k folds to a constant after
-// unrolling, so the switch reduces to one DPP move.
-__device__ __forceinline__ float row_bcast_dyn(float x, int k) {
-  switch (k) {
-    case 0: return row_bcast<0>(x);
-    case 1: return row_bcast<1>(x);
-    case 2: return row_bcast<2>(x);
-    case 3: return row_bcast<3>(x);
-    case 4: return row_bcast<4>(x);
-    case 5: return row_bcast<5>(x);
-    case 6: return row_bcast<6>(x);
-    case 7: return row_bcast<7>(x);
-    case 8: return row_bcast<8>(x);
-    case 9: return row_bcast<9>(x);
-    case 10: return row_bcast<10>(x);
-    case 11: return row_bcast<11>(x);
-    case 12: return row_bcast<12>(x);
-    case 13: return row_bcast<13>(x);
-    case 14: return row_bcast<14>(x);
-    default: return row_bcast<15>(x);
-  }
-}
-
-template <int GP>
-__device__ __forceinline__ float owner_bcast(const float* x, int j, int hh) {
-  return row_bcast_dyn(x[owner_reg<GP>(hh)], owner_lane<GP>(j, hh));
-}
-
 // Reductions over the four 16-lane rows of a wave (every lane gets the result).
-#if TC_DECODE_PERMLANE
 // v_permlane16_swap(x, x) leaves rows (x0, x0, x2, x2) and (x1, x1, x3, x3) in its two
 // results, so their sum is x0 + x1 (x2 + x3) in every lane; permlane32 pairs the halves.
 __device__ __forceinline__ float pair16_sum(float x) {
@@ -215,16 +122,6 @@ __device__ __forceinline__ float pair32_max(float x) {
 }
 __device__ __forceinline__ float rows_sum(float x) { return pair32_sum(pair16_sum(x)); }
 __device__ __forceinline__ float rows_max(float x) { return pair32_max(pair16_max(x)); }
-#else
-__device__ __forceinline__ float rows_sum(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
-}
-__device__ __forceinline__ float rows_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
-}
-#endif
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -238,11 +135,13 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int32_t off) 
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// K/V rows of one 16-token iteration of a wave: rows at or past `end` read
-// as zero (their scores are masked), so no index clamping is needed.
+// K/V of one 16-token tile of a wave (lane l = 16 g + n): k[i] = token n,
+// dims 32 i + 8 g .. +8 (the A operand of QK block i); v[j] = token 4 g + j,
+// dims 8 n .. +8. Rows at or past `end` read as zero (their scores are
+// masked), so no index clamping is needed.
 struct Tile {
-  uint4 k[4];  // register j: token slot j ^ (c >> 2)
-  uint4 v[4];  // register j: token slot j
+  uint4 k[4];
+  uint4 v[4];
 };
 
 __device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char* vslab, int32_t row_k,
@@ -260,116 +159,78 @@ __device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char
   }
 }
 
-template <int DT, int GP>
-struct Stream {
-  static constexpr int NV = 4 * GP;                   // partial dots per lane per iteration
-  static constexpr int VPL = NV >= 16 ? NV / 16 : 1;  // scores owned per lane
-  float m[VPL];          // running max (log2 domain) of the lane's head(s), per row
-  float l[VPL];          // running sum of exp2(score - m) over the lane's token slot
-  float acc[GP][8];      // running p.v for the lane's 8 dims, every head
+typedef _Float16 mfma_h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 mfma_h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 mfma_b8 __attribute__((ext_vector_type(8)));
+typedef short mfma_s4 __attribute__((ext_vector_type(4)));
+typedef float mfma_f4 __attribute__((ext_vector_type(4)));
 
-  __device__ __forceinline__ void init() {
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) { m[i] = neg_inf(); l[i] = 0.f; }
-#pragma unroll
-    for (int hh = 0; hh < GP; ++hh)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[hh][e] = 0.f;
+template <int DT> struct DecodeMma;
+template <> struct DecodeMma<TC_DTYPE_F16> {
+  static __device__ __forceinline__ mfma_f4 qk(const uint4& a, const uint4& b, const mfma_f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mfma_h8, a), __builtin_bit_cast(mfma_h8, b), c,
+                                                  0, 0, 0);
   }
-
-  // One 16-token iteration; `valid` masks the lane's score(s).
-  __device__ __forceinline__ void step(const Tile& t, const uint32_t (&qw)[GP][4], bool valid, float scale_log2) {
-    using E = Elem<DT>;
-    float x[NV];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int hh = 0; hh < GP; ++hh) {
-        float d = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) d = E::dot2(word(t.k[j], w), qw[hh][w], d);
-        x[j * GP + hh] = d;
-      }
-    row_reduce_scatter<NV>(x);
-
-    float p[VPL], alpha[VPL];
-    bool rescale = false;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const float s = valid ? x[i] * scale_log2 : neg_inf();
-      const float mn = fmaxf(m[i], head_max(s));
-      const float ms = (mn == neg_inf()) ? 0.f : mn;
-      p[i] = __builtin_amdgcn_exp2f(s - ms);
-      alpha[i] = __builtin_amdgcn_exp2f(m[i] - ms);
-      rescale |= (mn != m[i]) && (m[i] != neg_inf());
-      l[i] = l[i] * alpha[i] + p[i];
-      m[i] = mn;
-    }
-    if (__any(rescale)) {
-#pragma unroll
-      for (int hh = 0; hh < GP; ++hh) {
-        const float ah = owner_bcast<GP>(alpha, 0, hh);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[hh][e] *= ah;
-      }
-    }
-
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float vf[8];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        vf[2 * w] = E::lo(word(t.v[j], w));
-        vf[2 * w + 1] = E::hi(word(t.v[j], w));
-      }
-#pragma unroll
-      for (int hh = 0; hh < GP; ++hh) {
-        const float pj = owner_bcast<GP>(p, j, hh);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(pj, vf[e], acc[hh][e]);
-      }
-    }
+  static __device__ __forceinline__ mfma_f4 pv(const uint2& a, const uint2& b, const mfma_f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(mfma_h4, a), __builtin_bit_cast(mfma_h4, b), c,
+                                                 0, 0, 0);
+  }
+  // Two fp32 values rounded to nearest even into one word (first in the low half).
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 v = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct DecodeMma<TC_DTYPE_BF16> {
+  static __device__ __forceinline__ mfma_f4 qk(const uint4& a, const uint4& b, const mfma_f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mfma_b8, a), __builtin_bit_cast(mfma_b8, b), c,
+                                                   0, 0, 0);
+  }
+  static __device__ __forceinline__ mfma_f4 pv(const uint2& a, const uint2& b, const mfma_f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(mfma_s4, a), __builtin_bit_cast(mfma_s4, b),
+                                                     c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 v = {static_cast<__bf16>(x), static_cast<__bf16>(y)};
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 
-template <int DT, int GP>
+// V^T row of dim d in a wave's LDS region, in 32-bit words: 16 tokens (8
+// words) per row plus 4 words every 8 rows. The transposing 8-byte stores
+// (8 dims apart per lane) and the 8-byte A-operand reads (16 consecutive
+// dims) then hit distinct banks in each half-wave.
+__host__ __device__ constexpr int vt_word(int d) { return 8 * d + 4 * (d >> 3); }
+constexpr int kVtWords = vt_word(kHeadDim);   // per wave
+constexpr float kLazyMax = 8.f;               // log2 units the running maximum may lag
+
+template <int DT>
 __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const PartialArgs a) {
-  __shared__ float s_acc[kWaves][GP][kHeadDim];
-  __shared__ float s_m[kWaves][GP];
-  __shared__ float s_l[kWaves][GP];
+  using M = DecodeMma<DT>;
+  using E = Elem<DT>;
+  __shared__ uint32_t s_vt[kWaves][kVtWords];
+  __shared__ float s_acc[kWaves][8][kHeadDim];
+  __shared__ float s_m[kWaves][8];
+  __shared__ float s_l[kWaves][8];
 
   const int lane = threadIdx.x & 63;
-  // Wave-uniform by construction; readfirstlane lets the compiler keep the
-  // token range (and so the buffer resources) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = lane >> 4;
-  const int c = lane & 15;
+  const int n = lane & 15;   // head column (also the token row of the K operand)
+  const int g = lane >> 4;   // lane group
   const int split = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
 
-  // Cached tokens attended. Lengths past the buffer (or negative) are clamped
-  // into [0, n]. With an append the new token is one more, read from
-  // k_new/v_new and written to row `len`, so len stays below n: n - 1
-  // without lengths, lens[b] (the append position) clamped to n - 1 with.
-  // Token positions are 32-bit (the host keeps n and S * T below 2^30), and
-  // nothing before the first K/V requests divides: every wave runs this
-  // prologue before its first load, so its length is latency.
   const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
   const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
   const int32_t row_k = static_cast<int32_t>(a.sk_t) * 2, row_v = static_cast<int32_t>(a.sv_t) * 2;
-  // Materialise the slab addresses here so their kernel arguments are fetched
-  // with the others at entry (one scalar round trip instead of two).
   __asm__ volatile("" ::"s"(kslab), "s"(vslab));
-  const int32_t n = static_cast<int32_t>(a.n);
-  const int32_t len_cap = a.k_new ? n - 1 : n;
+  const int32_t nt = static_cast<int32_t>(a.n);
+  const int32_t len_cap = a.k_new ? nt - 1 : nt;
   int32_t len = len_cap;
   if (a.lens) len = min(max(a.lens[b], 0), len_cap);
-  // The wave's 16-token tiles start at tok and advance by tok_step while
-  // below end. Contiguous: split s, wave w own [s*T + w*T/W, s*T + (w+1)*T/W).
-  // Interleaved: all S*W waves of a head sweep the cache together, wave g
-  // taking tiles g, g + S*W, ..., so the loads in flight at any moment are
-  // adjacent in HBM.
   int32_t tok, tok_step, end;
   if (a.interleave) {
     tok = (split * kWaves + wave) * kWaveIter;
@@ -382,40 +243,87 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     end = min(tok + wave_tokens, len);
   }
 
+  // K: token n of the tile, bytes [64 i + 16 g, +16) for block i.
+  // V: tokens 4g + j, dims 8n .. 8n + 7.
   int32_t koff[4], voff[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    koff[j] = (4 * (j ^ (c >> 2)) + grp) * row_k + 16 * c;
-    voff[j] = (4 * j + grp) * row_v + 16 * c;
+  for (int i = 0; i < 4; ++i) {
+    koff[i] = n * row_k + 64 * i + 16 * g;
+    voff[i] = (4 * g + i) * row_v + 16 * n;
   }
-  // Ring of kDepth tiles, the first kDepth - 1 requested before anything
-  // else. Loads past `end` read nothing (the buffer range is empty there).
   Tile t[kDepth];
 #pragma unroll
   for (int d = 0; d < kDepth - 1; ++d)
     load_tile(t[d], kslab, vslab, row_k, row_v, tok + d * tok_step, end, koff, voff);
 
-  // The lane's 8 dims of every query row, in the lane's head order.
-  uint32_t qw[GP][4];
+  // Q as the B operand: head n, dims 32 i + 8 g .. +8 (zero for n >= G).
+  uint4 qb[4];
   {
-    const uint16_t* qb = a.q + b * a.sq_b + h * a.sq_h + 8 * c;
-    const int hp = head_perm<GP>(c);
+    const uint16_t* qrow = a.q + b * a.sq_b + h * a.sq_h + n * a.sq_g + 8 * g;
 #pragma unroll
-    for (int hh = 0; hh < GP; ++hh) {
-      const int row = hh ^ hp;
-      uint4 q4 = make_uint4(0u, 0u, 0u, 0u);
-      if (row < a.group) q4 = *reinterpret_cast<const uint4*>(qb + row * a.sq_g);
-      qw[hh][0] = q4.x; qw[hh][1] = q4.y; qw[hh][2] = q4.z; qw[hh][3] = q4.w;
+    for (int i = 0; i < 4; ++i) {
+      qb[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (n < a.group) qb[i] = *reinterpret_cast<const uint4*>(qrow + 32 * i);
     }
   }
 
-  Stream<DT, GP> st;
-  st.init();
-  const int my_slot = 4 * (c >> 2) + grp;  // token slot of the lane's score(s)
+  uint32_t* vt = s_vt[wave];
+  mfma_f4 acc[8];
+#pragma unroll
+  for (int bm = 0; bm < 8; ++bm) acc[bm] = mfma_f4{0.f, 0.f, 0.f, 0.f};
+  float m = neg_inf(), l = 0.f;
+
+  // One 16-token tile whose first token is t0 (tokens >= lim are masked).
+  auto step = [&](const Tile& tl, int32_t t0, int32_t lim) {
+    // S^T block: two independent chains of two MFMAs each.
+    mfma_f4 s0 = M::qk(tl.k[0], qb[0], mfma_f4{0.f, 0.f, 0.f, 0.f});
+    mfma_f4 s1 = M::qk(tl.k[1], qb[1], mfma_f4{0.f, 0.f, 0.f, 0.f});
+    s0 = M::qk(tl.k[2], qb[2], s0);
+    s1 = M::qk(tl.k[3], qb[3], s1);
+    // V^T rows into LDS while the matrix core works.
+    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&tl.v[0]);
+    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&tl.v[1]);
+    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&tl.v[2]);
+    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&tl.v[3]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t x01 = __builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel);
+      const uint32_t x23 = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);
+      *reinterpret_cast<uint2*>(vt + vt_word(8 * n + e) + 2 * g) = make_uint2(x01, x23);
+    }
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      x[r] = (t0 + 4 * g + r < lim) ? (s0[r] + s1[r]) * a.scale_log2 : neg_inf();
+    const float tmax = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+    // Lazy running maximum: moves only when the tile's exceeds it by kLazyMax.
+    const float mn = (tmax > m + kLazyMax || m == neg_inf()) ? tmax : m;
+    const float ms = (mn == neg_inf()) ? 0.f : mn;
+    if (__any(mn != m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);  // 0 while nothing was seen
+#pragma unroll
+      for (int bm = 0; bm < 8; ++bm) acc[bm] *= alpha;
+      l *= alpha;
+    }
+    m = mn;
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - ms);
+    l += (p[0] + p[1]) + (p[2] + p[3]);
+    const uint32_t h01 = M::pack(p[0], p[1]), h23 = M::pack(p[2], p[3]);
+    const uint32_t r01 = M::pack(p[0] - E::lo(h01), p[1] - E::hi(h01));
+    const uint32_t r23 = M::pack(p[2] - E::lo(h23), p[3] - E::hi(h23));
+    const uint2 phi = make_uint2(h01, h23), plo = make_uint2(r01, r23);
+#pragma unroll
+    for (int bm = 0; bm < 8; ++bm) {
+      const uint2 av = *reinterpret_cast<const uint2*>(vt + vt_word(16 * bm + n) + 2 * g);
+      acc[bm] = M::pv(av, phi, acc[bm]);
+      acc[bm] = M::pv(av, plo, acc[bm]);
+    }
+  };
 
   if (tok < end) {
-    // Tile d of a round is computed while the next kDepth - 1 tiles are in
-    // flight (ring indices fold to constants when unrolled).
     for (;;) {
       bool done = false;
 #pragma unroll
@@ -423,7 +331,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
         if (!done) {
           load_tile(t[(d + kDepth - 1) % kDepth], kslab, vslab, row_k, row_v, tok + (kDepth - 1) * tok_step, end,
                     koff, voff);
-          st.step(t[d], qw, tok + my_slot < end, a.scale_log2);
+          step(t[d], tok, end);
           tok += tok_step;
           done = tok >= end;
         }
@@ -433,8 +341,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   }
 
   if (a.k_new && split == 0 && wave == 0) {
-    // The appended token, as a tile whose only row is slot 0 (the buffer range
-    // is one row, so the other slots read zero and are masked).
+    // The appended token as a tile whose only row is token 0 (the buffer
+    // range is one row, so the other rows read zero and are masked).
     const char* kn = reinterpret_cast<const char*>(a.k_new + b * a.skn_b + h * a.skn_h);
     const char* vn = reinterpret_cast<const char*>(a.v_new + b * a.svn_b + h * a.svn_h);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kn, kHeadDim * 2);
@@ -442,10 +350,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     Tile tn;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      tn.k[j] = bload16(rk, koff[j]);
-      tn.v[j] = bload16(rv, voff[j]);
+      tn.k[j] = bload16(rk, 64 * j + 16 * g + n * kHeadDim * 2);
+      tn.v[j] = bload16(rv, (4 * g + j) * kHeadDim * 2 + 16 * n);
     }
-    st.step(tn, qw, my_slot == 0, a.scale_log2);
+    step(tn, 0, 1);
     if (lane < 32) {
       const bool is_v = lane >= 16;
       const int chunk = 8 * (lane & 15);
@@ -456,39 +364,14 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     }
   }
 
-  constexpr int VPL = Stream<DT, GP>::VPL;
-  // Row totals of l over the four token slots of each head, then every
-  // head's (m, l) to every lane.
+  // The head's sum over the four lane groups; m is already common to them.
+  l = rows_sum(l);
+  if (n < a.group) {
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) st.l[i] = head_sum(st.l[i]);
-  float mh[GP], lh[GP];
-#pragma unroll
-  for (int hh = 0; hh < GP; ++hh) {
-    mh[hh] = owner_bcast<GP>(st.m, 0, hh);
-    lh[hh] = owner_bcast<GP>(st.l, 0, hh);
-  }
-
-  // Merge the four rows (lanes c, c+16, c+32, c+48 hold the same dims).
-#pragma unroll
-  for (int hh = 0; hh < GP; ++hh) {
-    const float M = rows_max(mh[hh]);
-    const float f = __builtin_amdgcn_exp2f(mh[hh] - ((M == neg_inf()) ? 0.f : M));
-    lh[hh] = rows_sum(lh[hh] * f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) st.acc[hh][e] = rows_sum(st.acc[hh][e] * f);
-    mh[hh] = M;
-  }
-
-  // Merge the waves through LDS and write this split's partial.
-  if (grp == 0) {
-#pragma unroll
-    for (int hh = 0; hh < GP; ++hh)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wave][hh][8 * c + e] = st.acc[hh][e];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int hh = 0; hh < GP; ++hh) { s_m[wave][hh] = mh[hh]; s_l[wave][hh] = lh[hh]; }
+    for (int bm = 0; bm < 8; ++bm)
+      *reinterpret_cast<float4*>(&s_acc[wave][n][16 * bm + 4 * g]) =
+          make_float4(acc[bm][0], acc[bm][1], acc[bm][2], acc[bm][3]);
+    if (g == 0) { s_m[wave][n] = m; s_l[wave][n] = l; }
   }
   __syncthreads();
 
@@ -496,10 +379,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   for (int idx = threadIdx.x; idx < a.group * kHeadDim; idx += 64 * kWaves) {
     const int hh = idx / kHeadDim;
     const int d = idx % kHeadDim;
-    float M = neg_inf();
+    float Mx = neg_inf();
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hh]);
-    const float Ms = (M == neg_inf()) ? 0.f : M;
+    for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, s_m[w][hh]);
+    const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
@@ -507,16 +390,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       L += s_l[w][hh] * f;
       O += s_acc[w][hh][d] * f;
     }
-    // L >= 1 whenever a token was seen (the maximum contributes exp2(0)), so
-    // the hardware reciprocal and log2 need no denormal or zero handling.
+    // L >= 1 whenever a token was seen (the maximum contributes exp2(0)).
     a.o_part[(part * a.group + hh) * kHeadDim + d] = L == 0.f ? 0.f : O * __builtin_amdgcn_rcpf(L);
     if (d == 0)
-      a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (M + __builtin_amdgcn_logf(L)) * kLn2;
+      a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (Mx + __builtin_amdgcn_logf(L)) * kLn2;
   }
 }
 
-// Combine: one 256-thread work-group per (sequence, kv head, query head,
-// 32-dim quarter). Thread (sl, dq) folds splits sl, sl + 32, ... of dims
+// Combine: one 256-thread work-group per (32-dim quarter, query head; kv
+// head; sequence), a 3-D grid. Thread (sl, dq) folds splits sl, sl + 32, ... of dims
 // 4*dq .. 4*dq+3 with a running (max, sum, weighted o); the 32 split lanes are
 // merged with wave shuffles and one LDS exchange. All loads are issued before
 // any is consumed, so a call costs one memory round trip.
@@ -562,13 +444,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const CombineArgs a
   const int sl = tid / kCombineQuads;
   const int G = a.group;
   const int S = a.splits;
-  const int64_t blk = blockIdx.x;
-  const int quarter = static_cast<int>(blk & 3);
-  const int64_t bhg = blk >> 2;
-  const int g = static_cast<int>(bhg % G);
-  const int64_t bh = bhg / G;
-  const int h = static_cast<int>(bh % a.heads);
-  const int64_t b = bh / a.heads;
+  // Grid (4 * G, heads, batch): no index division before the loads.
+  const int quarter = blockIdx.x & 3;
+  const int g = blockIdx.x >> 2;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * a.heads + h;
   const int dim0 = 32 * quarter + 4 * dq;
 
   const float* lse = a.lse_part + bh * S * G + g;
@@ -630,19 +511,10 @@ int check_common(int batch, int kv_heads, int group, int head_dim, int dtype) {
   return TC_OK;
 }
 
-template <int DT, int GP>
-hipError_t launch_partial_t(const PartialArgs& a, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_partial_kernel<DT, GP>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0,
-                     stream, a);
-  return hipGetLastError();
-}
-
 template <int DT>
 hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream) {
-  if (a.group <= 1) return launch_partial_t<DT, 1>(a, batch, stream);
-  if (a.group <= 2) return launch_partial_t<DT, 2>(a, batch, stream);
-  if (a.group <= 4) return launch_partial_t<DT, 4>(a, batch, stream);
-  return launch_partial_t<DT, 8>(a, batch, stream);
+  hipLaunchKernelGGL((decode_partial_kernel<DT>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0, stream, a);
+  return hipGetLastError();
 }
 
 // Split plan of a call: S splits of T tokens each (S * T >= n, T a multiple of
@@ -832,9 +704,7 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   a.heads = kv_heads;
   a.group = group;
   a.splits = num_splits;
-  const int64_t blocks = static_cast<int64_t>(batch) * kv_heads * group * 4;
-  if (blocks > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many (sequence, head) pairs");
-  const dim3 grid(static_cast<unsigned>(blocks));
+  const dim3 grid(4 * group, kv_heads, batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TC_DTYPE_F16)
     hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_F16>), grid, dim3(256), 0, s, a);
