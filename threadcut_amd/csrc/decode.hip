@@ -375,23 +375,34 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   }
   __syncthreads();
 
+  // Each thread merges two adjacent dims of one head (one pass for G <= 4).
   const int64_t part = (static_cast<int64_t>(b) * a.heads + h) * a.splits + split;
-  for (int idx = threadIdx.x; idx < a.group * kHeadDim; idx += 64 * kWaves) {
-    const int hh = idx / kHeadDim;
-    const int d = idx % kHeadDim;
-    float Mx = neg_inf();
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, s_m[w][hh]);
-    const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
-    float L = 0.f, O = 0.f;
+  for (int idx = threadIdx.x; idx < a.group * (kHeadDim / 2); idx += 64 * kWaves) {
+    const int hh = idx / (kHeadDim / 2);
+    const int d = 2 * (idx % (kHeadDim / 2));
+    float mw[kWaves], lw[kWaves];
+    float2 ow[kWaves];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float f = __builtin_amdgcn_exp2f(s_m[w][hh] - Ms);
-      L += s_l[w][hh] * f;
-      O += s_acc[w][hh][d] * f;
+      mw[w] = s_m[w][hh];
+      lw[w] = s_l[w][hh];
+      ow[w] = *reinterpret_cast<const float2*>(&s_acc[w][hh][d]);
+    }
+    float Mx = neg_inf();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, mw[w]);
+    const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
+    float L = 0.f, O0 = 0.f, O1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = __builtin_amdgcn_exp2f(mw[w] - Ms);
+      L += lw[w] * f;
+      O0 += ow[w].x * f;
+      O1 += ow[w].y * f;
     }
     // L >= 1 whenever a token was seen (the maximum contributes exp2(0)).
-    a.o_part[(part * a.group + hh) * kHeadDim + d] = L == 0.f ? 0.f : O * __builtin_amdgcn_rcpf(L);
+    const float inv = L == 0.f ? 0.f : __builtin_amdgcn_rcpf(L);
+    *reinterpret_cast<float2*>(a.o_part + (part * a.group + hh) * kHeadDim + d) = make_float2(O0 * inv, O1 * inv);
     if (d == 0)
       a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (Mx + __builtin_amdgcn_logf(L)) * kLn2;
   }
