@@ -434,13 +434,37 @@ __device__ __forceinline__ Acc4 merge(const Acc4& a, const Acc4& b) {
   return r;
 }
 
-__device__ __forceinline__ Acc4 shfl_xor(const Acc4& a, int mask) {
-  Acc4 r;
-  r.m = __shfl_xor(a.m, mask);
-  r.l = __shfl_xor(a.l, mask);
-  r.o = make_float4(__shfl_xor(a.o.x, mask), __shfl_xor(a.o.y, mask), __shfl_xor(a.o.z, mask),
-                    __shfl_xor(a.o.w, mask));
-  return r;
+// Merges of a lane's state with its partner's, without LDS: lane ^ 8 by DPP
+// row_ror:8; lanes ^ 16 and ^ 32 by v_permlane16/32_swap, whose two results
+// hold the pair's two states in every lane (merge is symmetric).
+__device__ __forceinline__ Acc4 merge_xor8(const Acc4& a) {
+  Acc4 p;
+  p.m = dpp<DPP_ROW_ROR8>(a.m);
+  p.l = dpp<DPP_ROW_ROR8>(a.l);
+  p.o = make_float4(dpp<DPP_ROW_ROR8>(a.o.x), dpp<DPP_ROW_ROR8>(a.o.y), dpp<DPP_ROW_ROR8>(a.o.z),
+                    dpp<DPP_ROW_ROR8>(a.o.w));
+  return merge(a, p);
+}
+
+template <bool ROW32>
+__device__ __forceinline__ void swap_pair(float x, float& lo, float& hi) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = ROW32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                       : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
+template <bool ROW32>
+__device__ __forceinline__ Acc4 merge_swap(const Acc4& a) {
+  Acc4 x, y;
+  swap_pair<ROW32>(a.m, x.m, y.m);
+  swap_pair<ROW32>(a.l, x.l, y.l);
+  swap_pair<ROW32>(a.o.x, x.o.x, y.o.x);
+  swap_pair<ROW32>(a.o.y, x.o.y, y.o.y);
+  swap_pair<ROW32>(a.o.z, x.o.z, y.o.z);
+  swap_pair<ROW32>(a.o.w, x.o.w, y.o.w);
+  return merge(x, y);
 }
 
 template <int DT>
@@ -481,9 +505,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const CombineArgs a
     acc = merge(acc, one);
   }
   // Split lanes inside the wave: lanes dq + 8 * k, k = 0..7.
-  acc = merge(acc, shfl_xor(acc, 8));
-  acc = merge(acc, shfl_xor(acc, 16));
-  acc = merge(acc, shfl_xor(acc, 32));
+  acc = merge_xor8(acc);
+  acc = merge_swap<false>(acc);
+  acc = merge_swap<true>(acc);
   if (lane < kCombineQuads) s_part[wave][lane] = acc;
   __syncthreads();
   if (tid < kCombineQuads) {
