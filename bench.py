@@ -16,7 +16,8 @@ Printed JSON line:
   heads folded, fp16, threadcut/attention.py:40-42) on the host cores;
 - splice: the 36-layer suffix splice (Split(2048, 8668, 5668), 14336-token
   caches, theta 1e6) in one launch, algorithmic GB/s (C of K and V read and
-  written);
+  written), with the reference's CPU splice (torch ops per layer) timed on the
+  host beside it;
 - prefill: the GQA-native prefill attention on a 2048-token chunk over the
   7716 tokens that splice keeps, a 300-token chunk over 9700, and a causal
   2048-token prompt, in TFLOP/s of the matrix cores next to the reference's
@@ -110,6 +111,34 @@ def cpu_baseline(n, seconds):
             "sample": f"{len(times)} single decode calls (q [1,32,1,128], K/V [1,8,{n},128] fp16) of the "
                       f"reference's CPU path (torch SDPA, query heads folded), median {t * 1e6:.1f} us/call",
             "us_per_call": round(t * 1e6, 2)}
+
+
+def cpu_splice_baseline(seconds, layers=4):
+    """The reference's CPU splice (torch ops per layer, threadcut/kv.py:20-25,83-92) on
+    `layers` of the 36 config layers, timed for about `seconds` and scaled to 36."""
+    import torch
+
+    from oracle.splice import splice_growing_torch
+    from threadcut_amd import workloads
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    s = workloads.SPLICE_SPLIT
+    ks, vs = workloads.layer_caches(1, layers, workloads.SPLICE_TOKENS)
+    inv = workloads.inv_freq(1e6)
+    splice_growing_torch(ks, vs, s.a, s.c0, s.c, inv)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        splice_growing_torch(ks, vs, s.a, s.c0, s.c, inv)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t36 = times[len(times) // 2] * LAYERS / layers
+    return {"value": round(splice_bytes(s.c) / t36 / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_splice": round(t36 * 1e6, 1),
+            "sample": f"{len(times)} splices of {layers} of the 36 layers ([1,8,{workloads.SPLICE_TOKENS},128] fp16, "
+                      f"{s}) with the reference's torch ops on the host, median scaled to 36 layers"}
 
 
 def bench_splice(dev, steps, warmup):
@@ -549,6 +578,8 @@ def main():
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(n, args.cpu_seconds)
+        if "splice" in line:
+            line["splice"]["cpu_baseline"] = cpu_splice_baseline(min(5.0, args.cpu_seconds))
     print(json.dumps(line))
 
 

@@ -18,6 +18,9 @@ Functions and the reference lines each restates:
   any write (the reference clones), n = a + c, other rows unchanged.
 - ``splice_copy``: threadcut/kv.py:34-41 — index_select of [0, a) ∪ [c0, c0+c),
   then shift of rows [a:] when c and gap.
+- ``splice_growing_torch``: threadcut/kv.py:20-25 and :83-92 as the reference
+  runs them on host tensors (torch ops, per layer): the CPU path that bench.py
+  times as the splice's baseline.
 
 Pins (tests/test_oracle_splice.py): ``rope_table`` against float64 cos/sin;
 ``shift_keys`` bit for bit against the reference's torch op sequence on the
@@ -27,7 +30,8 @@ RoPE from transformers' own rotary embedding); shift(0) = identity, per-pair
 norms preserved, shift(d1)∘shift(d2) ≈ shift(d1+d2); ``splice_growing``
 against ``splice_copy`` for Split(10,17,20) (overlapping) and
 Split(12,12,0) as in tests/test_core.py:104-121, against a per-row brute force,
-and with rows outside [a, a+c) checked unchanged.
+and with rows outside [a, a+c) checked unchanged; ``splice_growing_torch``
+bit for bit against ``splice_growing``.
 """
 import numpy as np
 
@@ -90,3 +94,32 @@ def splice_copy(keys, values, a, c0, c, cos=None, sin=None, dtype="float16"):
     if c and c0 != a:
         k[..., a:, :] = shift_keys(k[..., a:, :], cos, sin, dtype)
     return k, v
+
+
+def splice_growing_torch(kbufs, vbufs, a, c0, c, inv_freq):
+    """threadcut/kv.py:83-92 over every layer, in place, with torch on host tensors.
+
+    kbufs/vbufs: lists of [B, H, cap, D] fp16/bf16 CPU tensors. Per layer, as
+    the reference: K[a:a+c] <- shift_keys(K[c0:c0+c], -gap) (kv.py:20-25: fp32
+    k*cos(emb) + rotate_half(k)*sin(emb), cast back), V[a:a+c] <- clone of
+    V[c0:c0+c].
+    """
+    import torch
+
+    if not c:
+        return
+    gap = c0 - a
+    f = torch.as_tensor(inv_freq).float()
+    angle = -gap * f
+    emb = torch.cat((angle, angle))
+    cos, sin = emb.cos(), emb.sin()
+    half = f.numel()
+    for kb, vb in zip(kbufs, vbufs):
+        keys = kb[..., c0:c0 + c, :]
+        if gap:
+            kf = keys.float()
+            rot = torch.cat((-kf[..., half:], kf[..., :half]), dim=-1)
+            kb[..., a:a + c, :] = (kf * cos + rot * sin).to(keys.dtype)
+        else:
+            kb[..., a:a + c, :] = keys.clone()
+        vb[..., a:a + c, :] = vb[..., c0:c0 + c, :].clone()

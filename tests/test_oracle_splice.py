@@ -181,3 +181,18 @@ def test_planted_mistakes_are_caught(mutation):
     same = np.array_equal(kb[..., :a + c, :].view(np.uint16), ck.view(np.uint16)) and \
         np.array_equal(vb[..., :a + c, :].view(np.uint16), cv.view(np.uint16))
     assert not same
+
+
+@pytest.mark.parametrize("a,c0,c", [(10, 17, 20), (12, 12, 0), (5, 40, 24), (0, 3, 61)])
+def test_torch_restatement_matches_numpy_oracle(a, c0, c):
+    """The torch form of the reference's CPU splice (bench.py's splice baseline) is
+    bit-identical to the numpy restatement, including overlapping moves."""
+    inv = osp.default_inv_freq(1e6, 128)
+    cos, sin = osp.rope_table(-(c0 - a), inv)
+    k = torch.randn(1, 2, 64, 128, generator=torch.Generator().manual_seed(20)).half()
+    v = torch.randn(1, 2, 64, 128, generator=torch.Generator().manual_seed(21)).half()
+    kb, vb, _ = osp.splice_growing(k.numpy(), v.numpy(), 64, a, c0, c, cos, sin)
+    kt, vt = [k.clone()], [v.clone()]
+    osp.splice_growing_torch(kt, vt, a, c0, c, inv)
+    assert np.array_equal(kt[0].numpy().view(np.uint16), kb.view(np.uint16))
+    assert np.array_equal(vt[0].numpy().view(np.uint16), vb.view(np.uint16))
