@@ -216,3 +216,84 @@ def test_append_attention_writes_the_row_and_attends_over_it(gpu, n):
     assert torch.equal(kc.cpu(), k_ref) and torch.equal(vc.cpu(), v_ref)   # only row n - 1 changed
     ref = f64_ref(q, k_ref[:, :, :n], v_ref[:, :, :n])
     assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL
+
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_softmax_weights_are_not_rounded_to_the_element_type(gpu, dtype):
+    """Two visible tokens with weights 1 and p1 = e^(b1 - 4), b1 chosen so that p1 is far
+    from a value of the element type: the fp32 partial must keep that weight (the
+    matrix-core P.V adds the rounding residue of P as a second product). Rounded P
+    alone would be off by up to 2^-9 (bf16) or 2^-12 (fp16) relative; the bar is 1e-5."""
+    hkv, g, d, n = 8, 4, 128, 64
+    # b1 on the element type's grid in [3, 4) whose weight e^(b1 - 4) rounds worst.
+    cand = torch.arange(3.0, 4.0, 1 / 64, dtype=torch.float64).to(dtype).double().unique()
+    p1 = torch.exp(cand - 4.0)
+    err = (p1 - p1.to(dtype).double()).abs() / p1
+    b1 = float(cand[int(err.argmax())])
+    p1 = float(torch.exp(torch.tensor(b1 - 4.0, dtype=torch.float64)))
+    q = torch.zeros(1, hkv, g, d, dtype=dtype)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, hkv, n, d, dtype=dtype)
+    k[..., 0] = -64.0          # every other key: weight e^-68, nothing in fp32 next to 1
+    k[:, :, 5, 0] = 4.0
+    k[:, :, 9, 0] = b1
+    v = torch.zeros(1, hkv, n, d, dtype=dtype)
+    v[:, :, 5] = 1.0
+    v[:, :, 9] = -1.0
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    o = torch.empty((1, hkv, 1, g, d), dtype=torch.float32, device=gpu)
+    lse = torch.empty((1, hkv, 1, g), dtype=torch.float32, device=gpu)
+    lib = _lib.load()
+    rc = lib.tc_decode_partial(qd.data_ptr(), _lib.i64x3(*qd.stride()[:3]), kd.data_ptr(), _lib.i64x3(*kd.stride()[:3]),
+                               vd.data_ptr(), _lib.i64x3(*vd.stride()[:3]), None, n, 1, hkv, g, d,
+                               _lib.dtype_code(dtype), 1.0, 64, 1, o.data_ptr(), lse.data_ptr(), _lib.stream_of(gpu))
+    _lib.check(rc, "tc_decode_partial")
+    torch.cuda.synchronize()
+    want = (1.0 - p1) / (1.0 + p1)
+    assert (o.cpu().double() - want).abs().max().item() <= 1e-5
+    assert (lse.cpu().double() - (4.0 + np.log1p(p1))).abs().max().item() <= 1e-5
+
+
+def test_nan_past_the_length_is_never_read(gpu):
+    """Cache buffers hold NaN past the valid rows: views [..., :n, :] and per-sequence
+    lengths only ever read valid rows (the loads' buffer range ends there)."""
+    cap = 4096
+    g_ = torch.Generator().manual_seed(61)
+    kbuf = torch.full((3, 8, cap, 128), float("nan"), dtype=torch.float16)
+    vbuf = torch.full((3, 8, cap, 128), float("nan"), dtype=torch.float16)
+    lens = torch.tensor([1, 1000, 3001], dtype=torch.int32)
+    for b_, n_ in enumerate(lens.tolist()):
+        kbuf[b_, :, :n_] = torch.randn(8, n_, 128, generator=g_).half()
+        vbuf[b_, :, :n_] = torch.randn(8, n_, 128, generator=g_).half()
+    q = torch.randn(3, 32, 1, 128, generator=g_).half()
+    got = run_decode(q, kbuf, vbuf, gpu, lens=lens)
+    assert np.isfinite(got).all()
+    assert np.abs(got - f64_ref(q, kbuf, vbuf, lens=lens)).max() <= TOL
+    n = 1000
+    kd, vd = kbuf.to(gpu), vbuf.to(gpu)   # slice on the device: the view's rows past n are NaN
+    out = flash_decode.decode_attention_batched(q[1:2].to(gpu).reshape(1, 8, 4, 128), kd[1:2, :, :n],
+                                                vd[1:2, :, :n], SCALE)
+    torch.cuda.synchronize()
+    ref = f64_ref(q[1:2], kbuf[1:2, :, :n], vbuf[1:2, :, :n])
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL
+
+
+def test_append_bf16_eight_query_heads_per_kv_head(gpu):
+    """The fused append at g = 8 (64 query heads over 8 KV heads) in bf16."""
+    n, cap = 2500, 2600
+    q, k, v, _ = workloads.decode_inputs(62, n=cap, q_heads=64, dtype=torch.bfloat16)
+    g_ = torch.Generator().manual_seed(63)
+    k_new = torch.randn(1, 8, 1, 128, generator=g_).to(torch.bfloat16)
+    v_new = torch.randn(1, 8, 1, 128, generator=g_).to(torch.bfloat16)
+    kc, vc = k.to(gpu), v.to(gpu)
+    out = torch.empty((1, 8, 8, 128), dtype=torch.bfloat16, device=gpu)
+    flash_decode.decode_append_into(q.to(gpu).reshape(1, 8, 8, 128), kc, vc, k_new.to(gpu), v_new.to(gpu), n,
+                                    SCALE, out)
+    torch.cuda.synchronize()
+    k_ref, v_ref = k.clone(), v.clone()
+    k_ref[:, :, n - 1] = k_new[:, :, 0]
+    v_ref[:, :, n - 1] = v_new[:, :, 0]
+    assert torch.equal(kc.cpu(), k_ref) and torch.equal(vc.cpu(), v_ref)
+    ref = f64_ref(q, k_ref[:, :, :n], v_ref[:, :, :n])
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= 4e-3
