@@ -22,7 +22,7 @@ constexpr int kHalf = kHeadDim / 2;
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = kThreads / 8;
 #ifndef TC_SPLICE_UNROLL
-#define TC_SPLICE_UNROLL 4  // passes of loads a thread keeps in flight
+#define TC_SPLICE_UNROLL 1  // passes of loads a thread keeps in flight (1 measured best: most work-groups)
 #endif
 #ifndef TC_SPLICE_NT
 #define TC_SPLICE_NT 1      // non-temporal loads and stores (the strips are touched once)
