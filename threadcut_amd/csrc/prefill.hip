@@ -264,8 +264,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const int64_t key_end = a.causal ? min(a.n, past + last_tok + 1) : a.n;
   const int64_t t_begin = split * a.split_tiles;
   const int64_t nt = min((key_end + kKeys - 1) / kKeys, t_begin + a.split_tiles);
+  // The tile map row, eight classes a word: the 64 words from t_begin on sit
+  // one per lane and are read back with v_readlane (no memory access in the
+  // loop); farther words are loaded.
+  const int64_t wbase = t_begin >> 3;
+  uint32_t map_lo = 0, map_hi = 0;
+  if (tcls && (wbase + lane) * 8 < a.pitch) {
+    const uint64_t x = reinterpret_cast<const uint64_t*>(tcls)[wbase + lane];
+    map_lo = static_cast<uint32_t>(x);
+    map_hi = static_cast<uint32_t>(x >> 32);
+  }
+  auto map_word = [&](int64_t w) -> uint64_t {
+    const int64_t i = w - wbase;
+    if (i < 64) {
+      const int ii = static_cast<int>(i);
+      return static_cast<uint64_t>(__builtin_amdgcn_readlane(map_lo, ii)) |
+             (static_cast<uint64_t>(__builtin_amdgcn_readlane(map_hi, ii)) << 32);
+    }
+    return reinterpret_cast<const uint64_t*>(tcls)[w];
+  };
   auto tile_class = [&](int64_t t) -> int {
-    if (tcls) return tcls[t];
+    if (tcls) return static_cast<int>((map_word(t >> 3) >> (8 * (t & 7))) & 0xff);
     if (a.mask) return TILE_MIXED;
     const int64_t key0 = t * kKeys;
     if (key0 + kKeys > a.n) return TILE_MIXED;
@@ -273,14 +292,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     return TILE_FULL;
   };
   // First active tile at or after t (nt if none). With a map, eight classes
-  // are tested per 8-byte read (rows are 8-aligned and padded with SKIP).
+  // are tested per word (rows are 8-aligned and padded with SKIP).
   auto next_active = [&](int64_t t) -> int64_t {
     if (!tcls) {
       while (t < nt && tile_class(t) == TILE_SKIP) ++t;
       return t;
     }
     while (t < nt) {
-      const uint64_t w = *reinterpret_cast<const uint64_t*>(tcls + (t & ~int64_t(7))) >> (8 * (t & 7));
+      const uint64_t w = map_word(t >> 3) >> (8 * (t & 7));
       if (w) return min(nt, t + (__builtin_ctzll(w) >> 3));
       t = (t & ~int64_t(7)) + 8;
     }
@@ -324,6 +343,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
     // S^T of the tile for every row group: each K fragment read from LDS
     // feeds kGroups MFMAs; the two 32-key halves are independent chains.
+    // The K fragments are read four chunks ahead of their MFMAs; the
+    // scheduling barriers keep the compiler from pulling the reads back next
+    // to their use (it otherwise waits out each read's latency).
     float16v s[kGroups][2];
 #pragma unroll
     for (int rg = 0; rg < kGroups; ++rg)
@@ -331,14 +353,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) s[rg][kt][v] = 0.f;
+    {
+      auto kfrag = [&](int c, int kt) {
+        return *reinterpret_cast<const uint4*>(lk + (32 * kt + r32) * kKStride + 16 * c + 8 * hi);
+      };
+      uint4 kf[4][2];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+      for (int c = 0; c < 4; ++c) { kf[c][0] = kfrag(c, 0); kf[c][1] = kfrag(c, 1); }
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const uint4 ka = *reinterpret_cast<const uint4*>(lk + (32 * kt + r32) * kKStride + 16 * c + 8 * hi);
+      for (int c = 0; c < 8; ++c) {
+        const uint4 k0 = kf[c & 3][0], k1 = kf[c & 3][1];
+        if (c + 4 < 8) { kf[c & 3][0] = kfrag(c + 4, 0); kf[c & 3][1] = kfrag(c + 4, 1); }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int rg = 0; rg < kGroups; ++rg) s[rg][kt] = Mfma<DT>::mma(ka, qb[rg][c], s[rg][kt]);
+        for (int rg = 0; rg < kGroups; ++rg) {
+          s[rg][0] = Mfma<DT>::mma(k0, qb[rg][c], s[rg][0]);
+          s[rg][1] = Mfma<DT>::mma(k1, qb[rg][c], s[rg][1]);
+        }
       }
+    }
 
     uint4 pb[kGroups][2][2];
 #pragma unroll
@@ -416,19 +449,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     }
 
     // O^T += V^T . P^T: each V^T fragment read from LDS feeds kGroups MFMAs.
+    // The four fragments of the next 16-key step are read one step ahead.
+    {
+      auto vfrag = [&](int p, int dt) {
+        const uint16_t* vp = lv + vt_row(32 * dt + r32) * kVStride + 32 * (p >> 1) + 16 * (p & 1) + 4 * hi;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
+        const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
+        return make_uint4(lo.x, lo.y, up.x, up.y);
+      };
+      uint4 vf[2][4];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int dt = 0; dt < 4; ++dt) vf[0][dt] = vfrag(0, dt);
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2)
+      for (int p = 0; p < 4; ++p) {
+        if (p < 3) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const uint16_t* vp = lv + vt_row(32 * dt + r32) * kVStride + 32 * kt + 16 * c2 + 4 * hi;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-          const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
-          const uint4 va = make_uint4(lo.x, lo.y, up.x, up.y);
-#pragma unroll
-          for (int rg = 0; rg < kGroups; ++rg) o[rg][dt] = Mfma<DT>::mma(va, pb[rg][kt][c2], o[rg][dt]);
+          for (int dt = 0; dt < 4; ++dt) vf[(p + 1) & 1][dt] = vfrag(p + 1, dt);
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int rg = 0; rg < kGroups; ++rg)
+            o[rg][dt] = Mfma<DT>::mma(vf[p & 1][dt], pb[rg][p >> 1][p & 1], o[rg][dt]);
+      }
+    }
 
     if (more) store_stage(st, s_k[buf ^ 1], s_v[buf ^ 1]);
     __syncthreads();
