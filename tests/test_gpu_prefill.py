@@ -115,6 +115,24 @@ def test_key_splits_with_batches(gpu, splits):
     check(qb, kb, vb, mask=workloads.causal_mask(L, n, batch=b).to(gpu), splits=splits, label="split batch bf16")
 
 
+@pytest.mark.parametrize("splits", [1, 3])
+def test_long_masked_map_row(gpu, splits):
+    """A 40000-key mask (625 tiles) in one key range: a work-group holds the first 64
+    words (512 tiles) of its tile-map row in registers and loads the rest. FULL, SKIP
+    and MIXED runs cross that boundary; the split case starts ranges mid-row."""
+    L, n = 40, 40000
+    q, k, v = workloads.prefill_inputs(60 + splits, q_len=L, n=n, device=gpu)
+    g = torch.Generator().manual_seed(splits)
+    m = torch.zeros((1, 1, L, n), dtype=torch.bool)
+    m[..., :5000] = True                                   # FULL tiles
+    m[..., 30000:34000] = torch.rand((L, 4000), generator=g) < 0.3   # MIXED across tile 512
+    m[..., 36000:36100] = True                             # FULL past the register words
+    m[..., 39990:] = torch.rand((L, 10), generator=g) < 0.5  # the ragged last tile
+    m[..., 7, :] = False                                   # a row that sees nothing
+    out = check(q, k, v, mask=m.to(gpu), splits=splits, label=f"long map row splits={splits}")
+    assert torch.all(out[0, 7] == 0)
+
+
 def test_short_chunk_on_long_cache_uses_splits(gpu):
     """A few hundred new tokens on top of a 10k cache: too few query blocks to fill
     the GPU, so the keys are split."""
