@@ -641,9 +641,11 @@ constexpr int kMaxPrefillSplits = 16;
 constexpr int kMinSplitTiles = 4;    // keys per split: at least 256
 
 // Key splits of a call: 1 when the query blocks alone give every CU two
-// work-groups, else enough splits to do so (each at least kMinSplitTiles
-// tiles, at most kMaxPrefillSplits). requested > 0 overrides the choice.
-// Trailing empty splits are dropped: the result times its tiles covers n.
+// work-groups, else as many as still fit the CUs' two work-group slots in one
+// round (each split at least kMinSplitTiles tiles, at most kMaxPrefillSplits):
+// a work-group more than the slots would run in a second round and double the
+// call. requested > 0 overrides the choice. Trailing empty splits are dropped:
+// the result times its tiles covers n.
 int plan_splits(int batch, int64_t q_len, int64_t n, int group, int kv_heads, int requested, int64_t* split_tiles,
                 int* splits_out) {
   int64_t nblk, ntiles;
@@ -657,7 +659,7 @@ int plan_splits(int batch, int64_t q_len, int64_t n, int group, int kv_heads, in
     if (rc != TC_OK) return rc;
     // Work-groups resident per CU: one per wave slot of a SIMD (4 waves each).
     const int64_t wgs = nblk * kv_heads * batch, slots = TC_PREFILL_WAVES * static_cast<int64_t>(cus);
-    if (wgs < slots) s = (slots + wgs - 1) / wgs;
+    if (wgs < slots) s = slots / wgs;
     s = std::min<int64_t>(s, std::max<int64_t>(1, ntiles / kMinSplitTiles));
   }
   s = std::max<int64_t>(1, std::min<int64_t>({s, kMaxPrefillSplits, std::max<int64_t>(1, ntiles)}));
