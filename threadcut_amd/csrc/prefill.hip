@@ -92,6 +92,7 @@ struct PrefillArgs {
   float* o_part;            // splits > 1: [b, splits, L, hq, d] fp32, normalized per split
   float* lse_part;          // splits > 1: [b, splits, L, hq] log2-sum-exp of the split (-inf if empty)
   int kv_heads, causal, neg, splits;
+  int fold_cus;             // > 0: pair work items w and W-1-w on one CU (see the kernel), W <= 2 x this
   float c;                  // |scale| * log2(e)
 };
 
@@ -218,7 +219,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   // Work item (KV head fastest, then key split, query block, batch):
   // consecutive work-groups go to different XCDs round-robin, so with
   // 8 | kv_heads each XCD's L2 streams one head's K/V.
-  const int64_t wid = blockIdx.x;
+  // With C CUs and a grid of C < W <= 2C work-groups (two fit a CU), the
+  // dispatcher puts work-groups i and i + C on the same CU (measured on this
+  // part). When the work grows along the items (causal rows see more keys),
+  // fold_cus = C hands work-group i >= C item W-1-(i-C), so each CU runs item
+  // i next to item W-1-i and the CUs finish together. Only the speed depends
+  // on that placement.
+  int64_t wid = blockIdx.x;
+  if (a.fold_cus > 0 && wid >= a.fold_cus) wid = static_cast<int64_t>(gridDim.x) - 1 - (wid - a.fold_cus);
   const int h = static_cast<int>(wid % a.kv_heads);
   int64_t rest = wid / a.kv_heads;
   const int split = static_cast<int>(rest % a.splits);
@@ -820,6 +828,14 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
   a.pitch = map_pitch(ntiles);
   a.kv_heads = kv_heads;
   a.causal = causal ? 1 : 0;
+  a.fold_cus = 0;
+  if (splits == 1 && (causal || mask_dev)) {
+    // One round of two work-groups per CU with rows that see more keys further down.
+    int cus = 0;
+    if ((rc = current_device_cus(&cus)) != TC_OK) return rc;
+    const int64_t wgs = nblk * kv_heads * batch;
+    if (wgs > cus && wgs <= 2 * static_cast<int64_t>(cus)) a.fold_cus = cus;
+  }
   a.neg = scale < 0.f ? 1 : 0;
   a.c = static_cast<float>(std::fabs(static_cast<double>(scale)) * 1.4426950408889634);
   hipStream_t s = static_cast<hipStream_t>(stream);
