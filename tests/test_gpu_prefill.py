@@ -243,6 +243,19 @@ def test_workload_shape_vs_torch_route(gpu):
     assert (out.float() - ref).abs().max().item() <= TOL[q.dtype]
 
 
+def test_causal_prompt_at_full_grid(gpu):
+    """A causal 2048-token prompt (32/8 heads): 512 work-groups, so long and short query
+    blocks share CUs (the folded work order, with the causal longest-first order on top)."""
+    q, k, v = workloads.prefill_inputs(15, q_len=2048, n=2048, device=gpu)
+    print("case: causal prompt 2048", flush=True)
+    out = prefill.prefill_attention(q, k, v, None, SCALE, True)
+    outs = [torch_route(q[:, 8 * i:8 * i + 8].float(), k[:, 2 * i:2 * i + 2].float(),
+                        v[:, 2 * i:2 * i + 2].float(), None, True) for i in range(4)]
+    ref = torch.cat(outs, 2)
+    torch.cuda.synchronize()
+    assert (out.float() - ref).abs().max().item() <= TOL[q.dtype]
+
+
 def test_rejects(gpu):
     q, k, v = workloads.prefill_inputs(15, q_len=8, n=8, q_heads=12, kv_heads=4, device=gpu)
     assert not prefill.supports(q, k, None)
