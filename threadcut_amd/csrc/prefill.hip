@@ -408,10 +408,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 #pragma unroll
           for (int v = 0; v < 16; ++v) mx = fmaxf(mx, (vis >> (16 * kt + v)) & 1u ? s[rg][kt][v] : neg_inf());
       } else {
+        // Four independent max chains (fmax is exact in any order).
+        float m4[4] = {s[rg][0][0], s[rg][0][1], s[rg][0][2], s[rg][0][3]};
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[rg][kt][v]);
+          for (int v = kt ? 0 : 4; v < 16; ++v) m4[v & 3] = fmaxf(m4[v & 3], s[rg][kt][v]);
+        mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
       }
 
       // Running maximum, moved only when the tile's maximum exceeds it by
@@ -434,7 +437,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
       // P^T operand of half kt, chunk c2: accumulators 8*c2 .. 8*c2+7 are keys
       // 16*c2 + {4hi..4hi+3, 8+4hi..8+4hi+3} of the half, the order in which
-      // V^T is read. The row sum takes the rounded P, as the MFMA does.
+      // V^T is read. All 32 exponentials come first, in one block with no
+      // branch between them (a per-pair mask test would cut the block in 16
+      // and leave each exp waiting on its fma); the mask then clears the
+      // hidden keys in one branch. The row sum takes the rounded P, as the
+      // MFMA does, in two chains (one per 32-key half).
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[rg][kt][v] = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v], a.c, -ms));
+      if (cls != TILE_FULL) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) s[rg][kt][v] = (vis >> (16 * kt + v)) & 1u ? s[rg][kt][v] : 0.f;
+      }
+      float lh[2] = {0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -443,17 +461,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int v0 = 8 * c2 + 2 * j;
-            float p0 = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v0], a.c, -ms));
-            float p1 = __builtin_amdgcn_exp2f(fmaf(s[rg][kt][v0 + 1], a.c, -ms));
-            if (cls != TILE_FULL) {
-              p0 = (vis >> (16 * kt + v0)) & 1u ? p0 : 0.f;
-              p1 = (vis >> (16 * kt + v0 + 1)) & 1u ? p1 : 0.f;
-            }
-            w[j] = pack2<DT>(p0, p1);
-            l[rg] = Elem<DT>::dot2(w[j], kOnes<DT>, l[rg]);
+            w[j] = pack2<DT>(s[rg][kt][v0], s[rg][kt][v0 + 1]);
+            lh[kt] = Elem<DT>::dot2(w[j], kOnes<DT>, lh[kt]);
           }
           pb[rg][kt][c2] = make_uint4(w[0], w[1], w[2], w[3]);
         }
+      l[rg] += lh[0] + lh[1];
     }
 
     // O^T += V^T . P^T: each V^T fragment read from LDS feeds kGroups MFMAs.
