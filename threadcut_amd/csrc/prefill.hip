@@ -846,8 +846,8 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
     // One round of two work-groups per CU with rows that see more keys further down.
     int cus = 0;
     if ((rc = current_device_cus(&cus)) != TC_OK) return rc;
-    const int64_t wgs = nblk * kv_heads * batch;
-    if (wgs > cus && wgs <= 2 * static_cast<int64_t>(cus)) a.fold_cus = cus;
+    const int64_t wgs = nblk * kv_heads * batch, slots = TC_PREFILL_WAVES * static_cast<int64_t>(cus);
+    if (wgs > cus && wgs <= slots) a.fold_cus = cus;
   }
   a.neg = scale < 0.f ? 1 : 0;
   a.c = static_cast<float>(std::fabs(static_cast<double>(scale)) * 1.4426950408889634);
