@@ -19,8 +19,9 @@
 // The online softmax runs per query row in fp32, log2 domain, as
 // p = exp2(s * c - m) with c = |scale| * log2(e) (a negative scale flips the
 // sign bits of Q instead). The running maximum m moves only when a tile's
-// maximum exceeds it by more than 2^8, so the accumulators are rescaled
-// rarely.
+// maximum exceeds it by more than a factor 2^8, so the accumulators are
+// rescaled rarely. The K and V^T fragments are read from LDS ahead of the
+// MFMAs that use them.
 //
 // Every tile is classified for the whole work-group: SKIP (no row sees any
 // of its keys: not loaded), FULL (every row sees every key: no per-element
