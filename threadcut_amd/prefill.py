@@ -101,16 +101,18 @@ def prefill_attention(query, key, value, attention_mask=None, scale=None, is_cau
         mask_ptr, mask_strides = m.data_ptr(), _mask_strides(m)
     scale = scale if scale is not None else d ** -0.5
     lib = _lib.load()
-    s = int(splits) if splits else num_splits(b, q, n, hq, hkv)
-    ws_bytes = lib.tc_prefill_workspace_bytes(b, q, hq, s)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes else None
-    rc = lib.tc_prefill_attention(
-        query.data_ptr(), _strides(query, (0, 1, 2)), key.data_ptr(), _strides(key, (0, 1, 2), 2),
-        value.data_ptr(), _strides(value, (0, 1, 2), 2), mask_ptr, mask_strides,
-        None if tiles is None else tiles.data_ptr(), 0 if tiles is None else tiles.numel(), int(bool(is_causal)),
-        q, n, b, hq, hkv, d, _lib.dtype_code(query.dtype), float(scale), s,
-        None if ws is None else ws.data_ptr(), ws_bytes, out.data_ptr(), _strides(out, (0, 1, 2)),
-        _lib.stream_of(query.device))
+    # The library plans splits for the current device (its CU count).
+    with torch.cuda.device(query.device):
+        s = int(splits) if splits else num_splits(b, q, n, hq, hkv)
+        ws_bytes = lib.tc_prefill_workspace_bytes(b, q, hq, s)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device) if ws_bytes else None
+        rc = lib.tc_prefill_attention(
+            query.data_ptr(), _strides(query, (0, 1, 2)), key.data_ptr(), _strides(key, (0, 1, 2), 2),
+            value.data_ptr(), _strides(value, (0, 1, 2), 2), mask_ptr, mask_strides,
+            None if tiles is None else tiles.data_ptr(), 0 if tiles is None else tiles.numel(),
+            int(bool(is_causal)), q, n, b, hq, hkv, d, _lib.dtype_code(query.dtype), float(scale), s,
+            None if ws is None else ws.data_ptr(), ws_bytes, out.data_ptr(), _strides(out, (0, 1, 2)),
+            _lib.stream_of(query.device))
     _lib.check(rc, "tc_prefill_attention")
     return out
 
@@ -137,8 +139,9 @@ def mask_tiles(mask, q_heads, kv_heads):
     st = _mask_strides(m)
     if mb == 1:
         st[0] = 0
-    rc = lib.tc_prefill_mask_tiles(m.data_ptr(), st, mb, q, n, q_heads, kv_heads, tiles.data_ptr(), tiles.numel(),
-                                   _lib.stream_of(mask.device))
+    with torch.cuda.device(mask.device):
+        rc = lib.tc_prefill_mask_tiles(m.data_ptr(), st, mb, q, n, q_heads, kv_heads, tiles.data_ptr(),
+                                       tiles.numel(), _lib.stream_of(mask.device))
     _lib.check(rc, "tc_prefill_mask_tiles")
     _tile_cache = (weakref.ref(mask), key, tiles)
     return tiles
