@@ -446,6 +446,46 @@ def measure_decode_step(dev, n=10240, steps=40):
             "note": "random-init weights; the step includes every layer's projections, MLP and the LM head"}
 
 
+def measure_torch_reads(dev, n, reps=50):
+    """What torch's own kernels achieve on one layer's K/V at n tokens ([2, 8, n, 128] fp16, 36 distinct
+    buffers, each sequence captured as one graph): a device copy (reads and writes the bytes) and an
+    fp32-accumulating sum (reads them). A yardstick for the decode's streaming rate at this size."""
+    import torch
+
+    bufs = [torch.randn((2, HKV, n, D), device=dev, dtype=torch.float16) for _ in range(LAYERS)]
+    dsts = [torch.empty_like(b) for b in bufs]
+    sums = [torch.empty((), device=dev, dtype=torch.float32) for _ in range(LAYERS)]
+    nbytes = bufs[0].numel() * 2
+    out = {}
+    for name, fn, moved in (("copy", lambda: [d.copy_(b) for d, b in zip(dsts, bufs)], 2 * nbytes),
+                            ("sum", lambda: [o.copy_(torch.sum(b, dtype=torch.float32))
+                                             for o, b in zip(sums, bufs)], nbytes)):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps / LAYERS
+        out[name] = {"us_per_layer": round(us, 2), "GB/s": round(moved / us / 1e3, 1),
+                     "frac": round(moved / us / 1e3 / PEAK_GBS, 4)}
+    out["bytes_read_per_layer"] = nbytes
+    del bufs, dsts, sums
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_match(seconds=2.0):
     """Request split at a 131072-token cache: the native matcher vs the reference's numpy windows."""
     import numpy as np
@@ -571,6 +611,7 @@ def main():
         line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
         line["long_131072"] = {f"B{b}": measure_long(dev, b, max(10, args.steps // 10)) for b in (1, 4)}
         line["decode_append"] = measure_append(dev, n, max(20, args.steps // 4))
+        line["torch_kernels_same_bytes"] = measure_torch_reads(dev, n)
         line["match_split"] = measure_match()
         line["prefill"] = measure_prefill(dev, args.steps)
         line["decode_step_model"] = measure_decode_step(dev, n)
