@@ -64,7 +64,9 @@ def test_full_splice_36_layers(gpu):
 
 
 @pytest.mark.parametrize("s", [Split(10, 17, 20), Split(12, 12, 0), Split(0, 1, 4000), Split(100, 200, 3000),
-                               Split(100, 229, 3000), Split(5, 4000, 1001), Split(3, 9, 4992), Split(0, 0, 50)])
+                               Split(100, 229, 3000), Split(5, 4000, 1001), Split(3, 9, 4992), Split(0, 0, 50),
+                               Split(100, 700, 4000), Split(0, 512, 4400), Split(7, 518, 511),
+                               Split(0, 1000, 4001)])
 def test_overlapping_and_edge_splits(gpu, s):
     n = 5001
     ks, vs = workloads.layer_caches(21, 3, n)

@@ -30,6 +30,13 @@ constexpr int kRowsPerPass = kThreads / 8;
 constexpr int kUnroll = TC_SPLICE_UNROLL;
 constexpr int kTileRows = kRowsPerPass * kUnroll;  // rows per work-group tile
 constexpr int kMaxJobs = 128;                      // strips sets per launch (64 layers x K,V)
+#ifndef TC_SPLICE_ROUND_GAP
+#define TC_SPLICE_ROUND_GAP 512
+#endif
+// An overlapping move (gap < rows moved) with a gap of at least this many rows
+// runs as ceil(rows / gap) parallel launches instead of one sequential walk
+// per strip (which is throughput-bound at 36 layers; see tc_splice_rope).
+constexpr int64_t kRoundGap = TC_SPLICE_ROUND_GAP;
 
 struct SpliceArgs {
   const uint16_t* src[kMaxJobs];
@@ -260,9 +267,25 @@ int tc_splice_rope(void* const* k_layers_host, void* const* v_layers_host, int n
   if ((rc = check_ptrs("v_layers", v_layers_host, num_layers)) != TC_OK) return rc;
   if (c == 0 || c0 == a || num_layers == 0) return TC_OK;
   if (!cos_sin_host) return fail(TC_ERR_INVALID_ARGUMENT, "cos_sin table is null");
-  const bool overlap = (c0 - a) < c;
-  return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides, batch,
-                     heads, dtype, c0, a, c, true, overlap, cos_sin_host, static_cast<hipStream_t>(stream));
+  const int64_t gap = c0 - a;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (gap >= c)  // disjoint ranges: every row in parallel
+    return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
+                       batch, heads, dtype, c0, a, c, true, false, cos_sin_host, s);
+  if (gap < kRoundGap)  // overlapping, short gap: one work-group walks each strip in row order
+    return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
+                       batch, heads, dtype, c0, a, c, true, true, cos_sin_host, s);
+  // Overlapping with a long gap: rounds of gap rows, one launch each. Round r
+  // writes rows a + r gap .. and reads rows a + (r+1) gap .., disjoint ranges,
+  // so it runs in parallel; it overwrites only sources of round r - 1, which
+  // the stream order has finished reading.
+  for (int64_t r0 = 0; r0 < c; r0 += gap) {
+    const int rc = launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides,
+                               strides, batch, heads, dtype, c0 + r0, a + r0, min(gap, c - r0), true, false,
+                               cos_sin_host, s);
+    if (rc != TC_OK) return rc;
+  }
+  return TC_OK;
 }
 
 int tc_splice_copy(void* const* k_src_host, void* const* v_src_host, const int64_t src_strides[3], int64_t src_tokens,
