@@ -66,7 +66,9 @@ def test_full_splice_36_layers(gpu):
 @pytest.mark.parametrize("s", [Split(10, 17, 20), Split(12, 12, 0), Split(0, 1, 4000), Split(100, 200, 3000),
                                Split(100, 229, 3000), Split(5, 4000, 1001), Split(3, 9, 4992), Split(0, 0, 50),
                                Split(100, 700, 4000), Split(0, 512, 4400), Split(7, 518, 511),
-                               Split(0, 1000, 4001)])
+                               Split(0, 1000, 4001), Split(0, 32, 4000), Split(2, 34, 33), Split(3, 103, 4001),
+                               Split(0, 511, 4490), Split(50, 300, 4701), Split(1, 32, 4000), Split(0, 47, 4000),
+                               Split(1, 49, 4000), Split(0, 500, 4000), Split(0, 500, 4001), Split(9, 609, 4392)])
 def test_overlapping_and_edge_splits(gpu, s):
     n = 5001
     ks, vs = workloads.layer_caches(21, 3, n)
@@ -156,11 +158,12 @@ def test_shift_is_rotation_composition_fp16(gpu):
     assert (shifted - want).abs().max().item() <= 2 * 2 ** -8
 
 
-def test_bf16_splice(gpu):
+@pytest.mark.parametrize("s", [Split(100, 900, 1000), Split(100, 170, 1830), Split(4, 20, 1900)])
+def test_bf16_splice(gpu, s):
     ks, vs = workloads.layer_caches(25, 2, 2000, dtype=torch.bfloat16)
     inv = workloads.inv_freq(1e6)
     cache = growing_cache(ks, vs, gpu)
-    s = Split(100, 900, 1000)
+    print(f"case: {s}", flush=True)
     kv.splice(cache, s, inv)
     torch.cuda.synchronize()
     for i, layer in enumerate(cache.layers):

@@ -30,13 +30,19 @@ constexpr int kRowsPerPass = kThreads / 8;
 constexpr int kUnroll = TC_SPLICE_UNROLL;
 constexpr int kTileRows = kRowsPerPass * kUnroll;  // rows per work-group tile
 constexpr int kMaxJobs = 128;                      // strips sets per launch (64 layers x K,V)
-#ifndef TC_SPLICE_ROUND_GAP
-#define TC_SPLICE_ROUND_GAP 512
+#ifndef TC_SPLICE_CHAIN_MIN
+#define TC_SPLICE_CHAIN_MIN 48
 #endif
 // An overlapping move (gap < rows moved) with a gap of at least this many rows
-// runs as ceil(rows / gap) parallel launches instead of one sequential walk
-// per strip (which is throughput-bound at 36 layers; see tc_splice_rope).
-constexpr int64_t kRoundGap = TC_SPLICE_ROUND_GAP;
+// runs as gap independent chains per strip, one thread walking each
+// (splice_kernel with DEPTH > 0); shorter gaps walk each strip in row order
+// with one work-group. Chains win from about two work-groups per strip.
+constexpr int64_t kChainMin = TC_SPLICE_CHAIN_MIN;
+// Chain rows a thread loads before it stores them: 8 holds a whole chain of up
+// to 8 rows at 128 VGPRs; longer chains run faster with 16 (235 VGPRs) in
+// flight, shorter ones slower (occupancy).
+constexpr int kChainDepthShort = 8;
+constexpr int kChainDepthLong = 16;
 
 struct SpliceArgs {
   const uint16_t* src[kMaxJobs];
@@ -48,6 +54,7 @@ struct SpliceArgs {
   int heads;
   int rot_jobs;    // jobs [0, rot_jobs) are keys (rotated), the rest copied
   int sequential;  // 1: one work-group walks a whole strip in row order
+  int64_t chain;   // > 0: chain walk of a move whose gap (src_row0 - dst_row0) is chain
 };
 
 __device__ __forceinline__ uint4 load16(const uint16_t* p) {
@@ -95,7 +102,7 @@ __device__ __forceinline__ void rotate_pair(uint4& lo, uint4& hi, const float (&
   hi = make_uint4(wh[0], wh[1], wh[2], wh[3]);
 }
 
-template <int DT>
+template <int DT, int DEPTH>
 __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
   const int job = blockIdx.z;
   const int64_t bh = blockIdx.y;
@@ -114,6 +121,41 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
   for (int i = 0; i < 8; ++i) {
     cv[i] = a.cs[8 * u + i];
     sv[i] = a.cs[kHalf + 8 * u + i];
+  }
+
+  if constexpr (DEPTH > 0) {
+    // Chain walk. Destination row r takes source row r + gap, so the rows
+    // j, j + gap, j + 2 gap ... (j < gap) form a chain that reads and writes
+    // only its own rows: each row is read as the source of the chain's
+    // previous row and then overwritten by the next one's. A thread walks one
+    // chain's 16-byte chunks in order. The store to row r overwrites what the
+    // same thread loaded for row r - gap, whose value an earlier store of this
+    // thread has already consumed, so no other thread and no barrier is involved.
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kRowsPerPass + r_in;
+    if (j >= a.chain) return;
+    for (int64_t r0 = j; r0 < a.rows; r0 += DEPTH * a.chain) {
+      uint4 lo[DEPTH], hi[DEPTH];
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        const int64_t r = r0 + i * a.chain;
+        if (r < a.rows) {
+          const uint16_t* p = src + (a.src_row0 + r) * a.ss_t;
+          lo[i] = load16(p);
+          hi[i] = load16(p + kHalf);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        const int64_t r = r0 + i * a.chain;
+        if (r < a.rows) {
+          if (rot) rotate_pair<DT>(lo[i], hi[i], cv, sv);
+          uint16_t* p = dst + (a.dst_row0 + r) * a.ds_t;
+          store16(p, lo[i]);
+          store16(p + kHalf, hi[i]);
+        }
+      }
+    }
+    return;
   }
 
   int64_t row = a.sequential ? 0 : static_cast<int64_t>(blockIdx.x) * kTileRows;
@@ -179,12 +221,20 @@ int check_ptrs(const char* what, void* const* ptrs, int n) {
   return TC_OK;
 }
 
+template <int DEPTH>
+void launch_kernel(bool f16, dim3 grid, hipStream_t stream, const SpliceArgs& a) {
+  if (f16)
+    hipLaunchKernelGGL((splice_kernel<TC_DTYPE_F16, DEPTH>), grid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((splice_kernel<TC_DTYPE_BF16, DEPTH>), grid, dim3(kThreads), 0, stream, a);
+}
+
 // Launches the kernel over `layers` layers, K strips rotated when `rotate`;
 // vsrc == nullptr moves keys only.
 int launch_rows(void* const* ksrc, void* const* vsrc, void* const* kdst, void* const* vdst, int layers,
                 const int64_t* ss, const int64_t* ds, int batch, int heads, int dtype, int64_t src_row0,
                 int64_t dst_row0, int64_t rows, bool rotate, bool sequential, const float* cos_sin,
-                hipStream_t stream) {
+                hipStream_t stream, int64_t chain = 0) {
   if (rows <= 0 || layers <= 0) return TC_OK;
   constexpr int kLayersPerLaunch = kMaxJobs / 2;
   const int per_layer = vsrc ? 2 : 1;
@@ -209,14 +259,20 @@ int launch_rows(void* const* ksrc, void* const* vsrc, void* const* kdst, void* c
     a.heads = heads;
     a.rot_jobs = rotate ? nl : 0;
     a.sequential = sequential ? 1 : 0;
-    const int64_t tiles = sequential ? 1 : ceil_div(rows, kTileRows);
+    a.chain = chain;
+    const int64_t tiles = chain > 0 ? ceil_div(min(chain, rows), kRowsPerPass)
+                                    : sequential ? 1 : ceil_div(rows, kTileRows);
     if (tiles > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many rows (%lld)", (long long)rows);
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batch * heads),
                     static_cast<unsigned>(per_layer * nl));
-    if (dtype == TC_DTYPE_F16)
-      hipLaunchKernelGGL((splice_kernel<TC_DTYPE_F16>), grid, dim3(kThreads), 0, stream, a);
+    const int depth = chain <= 0 ? 0 : rows > kChainDepthShort * chain ? kChainDepthLong : kChainDepthShort;
+    const bool f16 = dtype == TC_DTYPE_F16;
+    if (depth == kChainDepthLong)
+      launch_kernel<kChainDepthLong>(f16, grid, stream, a);
+    else if (depth == kChainDepthShort)
+      launch_kernel<kChainDepthShort>(f16, grid, stream, a);
     else
-      hipLaunchKernelGGL((splice_kernel<TC_DTYPE_BF16>), grid, dim3(kThreads), 0, stream, a);
+      launch_kernel<0>(f16, grid, stream, a);
     const int rc = hip_status(hipGetLastError(), "splice launch");
     if (rc != TC_OK) return rc;
   }
@@ -272,20 +328,12 @@ int tc_splice_rope(void* const* k_layers_host, void* const* v_layers_host, int n
   if (gap >= c)  // disjoint ranges: every row in parallel
     return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
                        batch, heads, dtype, c0, a, c, true, false, cos_sin_host, s);
-  if (gap < kRoundGap)  // overlapping, short gap: one work-group walks each strip in row order
+  if (gap < kChainMin)  // overlapping, short gap: one work-group walks each strip in row order
     return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
                        batch, heads, dtype, c0, a, c, true, true, cos_sin_host, s);
-  // Overlapping with a long gap: rounds of gap rows, one launch each. Round r
-  // writes rows a + r gap .. and reads rows a + (r+1) gap .., disjoint ranges,
-  // so it runs in parallel; it overwrites only sources of round r - 1, which
-  // the stream order has finished reading.
-  for (int64_t r0 = 0; r0 < c; r0 += gap) {
-    const int rc = launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides,
-                               strides, batch, heads, dtype, c0 + r0, a + r0, min(gap, c - r0), true, false,
-                               cos_sin_host, s);
-    if (rc != TC_OK) return rc;
-  }
-  return TC_OK;
+  // Overlapping: gap independent chains per strip.
+  return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
+                     batch, heads, dtype, c0, a, c, true, false, cos_sin_host, s, gap);
 }
 
 int tc_splice_copy(void* const* k_src_host, void* const* v_src_host, const int64_t src_strides[3], int64_t src_tokens,
