@@ -43,6 +43,12 @@ constexpr int64_t kChainMin = TC_SPLICE_CHAIN_MIN;
 // flight, shorter ones slower (occupancy).
 constexpr int kChainDepthShort = 8;
 constexpr int kChainDepthLong = 16;
+// Dynamic LDS the row kernel is launched with and never touches: 26 KB of a
+// CU's 160 KB holds residency at 6 work-groups (24 waves) per CU instead of 8.
+// The parallel move of 36 layers x 5668 rows takes 282 us so against 290 us
+// at 8 per CU; 4 per CU measured the same as 8, 5 and 7 between, 3 and 2
+// far slower.
+constexpr unsigned kRowKernelLds = 26624;
 
 struct SpliceArgs {
   const uint16_t* src[kMaxJobs];
@@ -223,10 +229,11 @@ int check_ptrs(const char* what, void* const* ptrs, int n) {
 
 template <int DEPTH>
 void launch_kernel(bool f16, dim3 grid, hipStream_t stream, const SpliceArgs& a) {
+  const unsigned lds = DEPTH > 0 ? 0 : kRowKernelLds;
   if (f16)
-    hipLaunchKernelGGL((splice_kernel<TC_DTYPE_F16, DEPTH>), grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((splice_kernel<TC_DTYPE_F16, DEPTH>), grid, dim3(kThreads), lds, stream, a);
   else
-    hipLaunchKernelGGL((splice_kernel<TC_DTYPE_BF16, DEPTH>), grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((splice_kernel<TC_DTYPE_BF16, DEPTH>), grid, dim3(kThreads), lds, stream, a);
 }
 
 // Launches the kernel over `layers` layers, K strips rotated when `rotate`;
