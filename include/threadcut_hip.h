@@ -164,6 +164,28 @@ int tc_decode_append_attention_at(const void* q_dev, const int64_t q_strides[3],
                                   void* workspace_dev, size_t workspace_bytes,
                                   void* out_dev, const int64_t out_strides[3], void* stream);
 
+/* Decode over a paged cache. k_pool_dev / v_pool_dev are page pools
+ * [num_pages, kv_heads, page_tokens, head_dim] with element strides
+ * pool_strides = (page, head, token), shared by K and V. Sequence b attends
+ * to the keys of its tiles tile_table_dev[(b * max_tiles + i) * 4 ..],
+ * i < tiles_dev[b] (clamped to [0, max_tiles]): int32 {page, first slot,
+ * rows, 0}, rows <= 16 consecutive slots of one page. An entry whose page is
+ * outside [0, num_pages), whose rows are outside [0, 16] or whose slots run
+ * past page_tokens counts as empty. Attention over a set of keys does not
+ * depend on their order, so the tiles of a pruned sequence need no
+ * compaction. Workspace as tc_decode_attention(..., n_tokens =
+ * 16 * max_tiles, ragged = batch > 1). This is decode_attention
+ * (threadcut/flash_decode.py:57-69) over the paged KV with slot reuse that
+ * threadcut/README.md:141-144 names as the next step. */
+int tc_decode_paged_attention(const void* q_dev, const int64_t q_strides[3],
+                              const void* k_pool_dev, const void* v_pool_dev,
+                              const int64_t pool_strides[3], int num_pages, int page_tokens,
+                              const int32_t* tile_table_dev, const int32_t* tiles_dev,
+                              int64_t max_tiles, int batch, int kv_heads, int group,
+                              int head_dim, int dtype, float scale, int split_tokens,
+                              void* workspace_dev, size_t workspace_bytes,
+                              void* out_dev, const int64_t out_strides[3], void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* RoPE delta-shift and suffix splice                                        */
 /*                                                                           */
@@ -208,6 +230,21 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
                    int batch, int heads, int head_dim, int dtype,
                    int64_t a, int64_t c0, int64_t c,
                    const float* cos_sin_host, void* stream);
+
+/* The splice of a paged cache: the keys of the kept suffix are rotated in
+ * place by the angle table cos_sin_host (the shift of tc_shift_keys); V is
+ * not touched. For every layer's K pool (k_pools_host: HOST array of
+ * num_layers device pointers to pools laid out as in
+ * tc_decode_paged_attention) and every head, the rows of the num_tiles
+ * entries of tiles_dev (int32 {page, first slot, rows, 0}, the tile format of
+ * tc_decode_paged_attention) are rotated. Entries must not overlap (a row
+ * listed twice is rotated twice); invalid entries are skipped. With pages,
+ * dropping the pruned span frees its pages, so this replaces the suffix move
+ * of threadcut/kv.py:28-41,83-92, as threadcut/README.md:141-144 proposes. */
+int tc_paged_rotate_keys(void* const* k_pools_host, int num_layers, const int64_t pool_strides[3],
+                         int num_pages, int page_tokens, const int32_t* tiles_dev,
+                         int64_t num_tiles, int kv_heads, int head_dim, int dtype,
+                         const float* cos_sin_host, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Prefill attention                                                         */

@@ -51,10 +51,13 @@ SIGNATURES = {
                                         _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_decode_append_attention_at": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I,
                                            _I, _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
+    "tc_decode_paged_attention": (_I, [_P, _I64P, _P, _P, _I64P, _I, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
+                                       _P, _S, _P, _I64P, _P]),
     "tc_shift_keys": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I64, _I, _I, _FP, _P]),
     "tc_splice_rope": (_I, [_PP, _PP, _I, _I64P, _I, _I, _I64, _I, _I, _I64, _I64, _I64, _FP, _P]),
     "tc_splice_copy": (_I, [_PP, _PP, _I64P, _I64, _PP, _PP, _I64P, _I, _I, _I, _I, _I, _I64, _I64, _I64,
                             _FP, _P]),
+    "tc_paged_rotate_keys": (_I, [_PP, _I, _I64P, _I, _I, _P, _I64, _I, _I, _I, _FP, _P]),
     "tc_prefill_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _S, _I, _I64, _I64, _I, _I,
                                   _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_prefill_num_splits": (_I, [_I, _I64, _I64, _I, _I]),

@@ -91,6 +91,15 @@ struct PartialArgs {
   int64_t skn_b, skn_h, svn_b, svn_h;
   uint16_t* k_w;
   uint16_t* v_w;
+  // Paged cache (decode_partial_kernel<DT, true>): k and v are page pools
+  // [pages, H, P, D] with element strides (sk_b, sk_h, sk_t) = (page, head,
+  // token). Sequence b's keys are the tiles tile_tab[b * max_tiles + i],
+  // i < tiles[b], each {page, first slot, rows, 0}: rows (<= 16) consecutive
+  // slots of one page. Entries outside the pool or the page count as empty.
+  const int32_t* tile_tab;
+  const int32_t* tiles;
+  int64_t max_tiles;
+  int32_t pages, page_tokens;
 };
 
 struct CombineArgs {
@@ -142,6 +151,7 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int32_t off) 
 struct Tile {
   uint4 k[4];
   uint4 v[4];
+  int32_t rows;  // paged cache: the tile's key rows (the rest read as zero)
 };
 
 __device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char* vslab, int32_t row_k,
@@ -152,6 +162,26 @@ __device__ __forceinline__ void load_tile(Tile& t, const char* kslab, const char
   const int32_t rows = __builtin_amdgcn_readfirstlane(min(max(end - t0, 0), 16));
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kslab + static_cast<int64_t>(t0) * row_k, rows * row_k);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vslab + static_cast<int64_t>(t0) * row_v, rows * row_v);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    t.k[j] = bload16(rk, koff[j]);
+    t.v[j] = bload16(rv, voff[j]);
+  }
+}
+
+// Paged cache: rows (<= 16) key rows from slot `slot` of page `page`. The
+// buffer range spans exactly those rows, so the rest of the tile reads as
+// zero; an entry outside the pool or past the page's end loads nothing.
+__device__ __forceinline__ void load_paged_tile(Tile& t, const char* kpool, const char* vpool, int32_t row_k,
+                                                int32_t row_v, int64_t page_k, int64_t page_v, int32_t pages,
+                                                int32_t page_tokens, int32_t page, int32_t slot, int32_t rows,
+                                                const int32_t* koff, const int32_t* voff) {
+  if (page < 0 || page >= pages || slot < 0 || rows < 0 || rows > 16 || slot > page_tokens - rows) {
+    page = 0; slot = 0; rows = 0;
+  }
+  t.rows = rows;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kpool + page * page_k + static_cast<int64_t>(slot) * row_k, rows * row_k);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vpool + page * page_v + static_cast<int64_t>(slot) * row_v, rows * row_v);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     t.k[j] = bload16(rk, koff[j]);
@@ -206,7 +236,7 @@ __host__ __device__ constexpr int vt_word(int d) { return 8 * d + 4 * (d >> 3); 
 constexpr int kVtWords = vt_word(kHeadDim);   // per wave
 constexpr float kLazyMax = 8.f;               // log2 units the running maximum may lag
 
-template <int DT>
+template <int DT, bool PAGED>
 __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const PartialArgs a) {
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
@@ -223,14 +253,22 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   const int h = blockIdx.y;
   const int b = blockIdx.z;
 
-  const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
-  const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
+  // Paged: the pools' head slabs, pages added per tile; otherwise sequence b's slabs.
+  const char* kslab = reinterpret_cast<const char*>(a.k + (PAGED ? 0 : b * a.sk_b) + h * a.sk_h);
+  const char* vslab = reinterpret_cast<const char*>(a.v + (PAGED ? 0 : b * a.sv_b) + h * a.sv_h);
   const int32_t row_k = static_cast<int32_t>(a.sk_t) * 2, row_v = static_cast<int32_t>(a.sv_t) * 2;
   __asm__ volatile("" ::"s"(kslab), "s"(vslab));
   const int32_t nt = static_cast<int32_t>(a.n);
   const int32_t len_cap = a.k_new ? nt - 1 : nt;
   int32_t len = len_cap;
-  if (a.lens) len = min(max(a.lens[b], 0), len_cap);
+  const int32_t* tab = nullptr;
+  if constexpr (PAGED) {
+    // Token index space of 16 per tile; a tile's own row count masks the rest.
+    len = 16 * min(max(a.tiles[b], 0), static_cast<int32_t>(a.max_tiles));
+    tab = a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4;
+  } else if (a.lens) {
+    len = min(max(a.lens[b], 0), len_cap);
+  }
   int32_t tok, tok_step, end;
   if (a.interleave) {
     tok = (split * kWaves + wave) * kWaveIter;
@@ -251,10 +289,40 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     koff[i] = n * row_k + 64 * i + 16 * g;
     voff[i] = (4 * g + i) * row_v + 16 * n;
   }
+  // Paged: lane i holds the table entry of the wave's i-th tile; tiles past
+  // the 64th read theirs from memory.
+  int32_t e_page = 0, e_slot = 0, e_rows = 0;
+  if constexpr (PAGED) {
+    const int32_t ti = tok + lane * tok_step;
+    if (ti < end) {
+      const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (ti >> 4));
+      e_page = e.x; e_slot = e.y; e_rows = e.z;
+    }
+  }
+  int32_t li = 0;  // the wave's tiles loaded so far
+  auto load = [&](Tile& tl, int32_t t0) {
+    if constexpr (PAGED) {
+      int32_t page = 0, slot = 0, rows = 0;
+      if (li < 64) {
+        page = __builtin_amdgcn_readlane(e_page, li);
+        slot = __builtin_amdgcn_readlane(e_slot, li);
+        rows = __builtin_amdgcn_readlane(e_rows, li);
+      } else if (t0 < end) {
+        const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (t0 >> 4));
+        page = __builtin_amdgcn_readfirstlane(e.x);
+        slot = __builtin_amdgcn_readfirstlane(e.y);
+        rows = __builtin_amdgcn_readfirstlane(e.z);
+      }
+      ++li;
+      load_paged_tile(tl, kslab, vslab, row_k, row_v, a.sk_b * 2, a.sv_b * 2, a.pages, a.page_tokens, page, slot,
+                      rows, koff, voff);
+    } else {
+      load_tile(tl, kslab, vslab, row_k, row_v, t0, end, koff, voff);
+    }
+  };
   Tile t[kDepth];
 #pragma unroll
-  for (int d = 0; d < kDepth - 1; ++d)
-    load_tile(t[d], kslab, vslab, row_k, row_v, tok + d * tok_step, end, koff, voff);
+  for (int d = 0; d < kDepth - 1; ++d) load(t[d], tok + d * tok_step);
 
   // Q as the B operand: head n, dims 32 i + 8 g .. +8 (zero for n >= G).
   uint4 qb[4];
@@ -329,9 +397,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
 #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
         if (!done) {
-          load_tile(t[(d + kDepth - 1) % kDepth], kslab, vslab, row_k, row_v, tok + (kDepth - 1) * tok_step, end,
-                    koff, voff);
-          step(t[d], tok, end);
+          load(t[(d + kDepth - 1) % kDepth], tok + (kDepth - 1) * tok_step);
+          step(t[d], tok, PAGED ? tok + t[d].rows : end);
           tok += tok_step;
           done = tok >= end;
         }
@@ -548,7 +615,12 @@ int check_common(int batch, int kv_heads, int group, int head_dim, int dtype) {
 
 template <int DT>
 hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_partial_kernel<DT>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0, stream, a);
+  if (a.tile_tab)
+    hipLaunchKernelGGL((decode_partial_kernel<DT, true>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0, stream,
+                       a);
+  else
+    hipLaunchKernelGGL((decode_partial_kernel<DT, false>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0,
+                       stream, a);
   return hipGetLastError();
 }
 
@@ -633,10 +705,19 @@ struct Append {
   void* v_cache;
 };
 
+// A paged cache: the tile table of every sequence and the pool's shape.
+struct Paged {
+  const int32_t* tile_tab;  // [B, max_tiles, 4]
+  const int32_t* tiles;     // [B]
+  int64_t max_tiles;
+  int pages, page_tokens;
+};
+
 int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
                  const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens, int batch,
                  int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens, int num_splits,
-                 float* o_part_dev, float* lse_part_dev, int interleave, const Append* app, void* stream) {
+                 float* o_part_dev, float* lse_part_dev, int interleave, const Append* app, void* stream,
+                 const Paged* paged = nullptr) {
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens == 0 && num_splits == 0) return TC_OK;  // empty caches: nothing to read
@@ -695,6 +776,11 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.k_w = app ? static_cast<uint16_t*>(app->k_cache) : nullptr;
   a.v_w = app ? static_cast<uint16_t*>(app->v_cache) : nullptr;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  a.tile_tab = paged ? paged->tile_tab : nullptr;
+  a.tiles = paged ? paged->tiles : nullptr;
+  a.max_tiles = paged ? paged->max_tiles : 0;
+  a.pages = paged ? paged->pages : 0;
+  a.page_tokens = paged ? paged->page_tokens : 0;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, s)
@@ -757,7 +843,7 @@ int attention_impl(const void* q_dev, const int64_t q_strides[3], const void* k_
                    const void* v_dev, const int64_t v_strides[3], const int32_t* lens_dev, int64_t n_tokens,
                    int batch, int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
                    void* workspace_dev, size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
-                   const Append* app, int ragged_plan, void* stream) {
+                   const Append* app, int ragged_plan, void* stream, const Paged* paged = nullptr) {
   int rc = check_common(batch, kv_heads, group, head_dim, dtype);
   if (rc != TC_OK) return rc;
   if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
@@ -771,7 +857,7 @@ int attention_impl(const void* q_dev, const int64_t q_strides[3], const void* k_
   if (S > 0) {
     // Splits here are internal, so their tiles are dealt round-robin (the merged result is the same).
     rc = partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
-                      head_dim, dtype, scale, t, S, o_part, lse_part, TC_DECODE_INTERLEAVE, app, stream);
+                      head_dim, dtype, scale, t, S, o_part, lse_part, TC_DECODE_INTERLEAVE, app, stream, paged);
     if (rc != TC_OK) return rc;
   }
   return tc_decode_combine(o_part, lse_part, batch, kv_heads, group, head_dim, S, out_dev, out_strides, dtype, stream);
@@ -837,6 +923,30 @@ int tc_decode_append_attention_at(const void* q_dev, const int64_t q_strides[3],
   return append_impl(q_dev, q_strides, k_cache_dev, k_strides, v_cache_dev, v_strides, k_new_dev, k_new_strides,
                      v_new_dev, v_new_strides, pos_dev, capacity, batch, kv_heads, group, head_dim, dtype, scale,
                      split_tokens, workspace_dev, workspace_bytes, out_dev, out_strides, stream);
+}
+
+int tc_decode_paged_attention(const void* q_dev, const int64_t q_strides[3], const void* k_pool_dev,
+                              const void* v_pool_dev, const int64_t pool_strides[3], int num_pages, int page_tokens,
+                              const int32_t* tile_table_dev, const int32_t* tiles_dev, int64_t max_tiles, int batch,
+                              int kv_heads, int group, int head_dim, int dtype, float scale, int split_tokens,
+                              void* workspace_dev, size_t workspace_bytes, void* out_dev,
+                              const int64_t out_strides[3], void* stream) {
+  clear_error();
+  if (num_pages < 1 || page_tokens < 1)
+    return fail(TC_ERR_INVALID_ARGUMENT, "pool of %d pages of %d tokens", num_pages, page_tokens);
+  if (max_tiles < 0 || max_tiles > kMaxTokens / 16)
+    return fail(TC_ERR_INVALID_ARGUMENT, "max_tiles %lld outside [0, %lld]", (long long)max_tiles,
+                (long long)(kMaxTokens / 16));
+  if (max_tiles > 0 && (!tile_table_dev || !tiles_dev)) return fail(TC_ERR_INVALID_ARGUMENT, "null tile table");
+  if (max_tiles > 0 && !aligned16(tile_table_dev))
+    return fail(TC_ERR_ALIGNMENT, "tile table not 16-byte aligned");
+  if (!pool_strides) return fail(TC_ERR_INVALID_ARGUMENT, "null pool strides");
+  // An empty table plans zero splits, so the partial kernel (the only reader
+  // of the table) is not launched.
+  const Paged p{tile_table_dev, tiles_dev, max_tiles, num_pages, page_tokens};
+  return attention_impl(q_dev, q_strides, k_pool_dev, pool_strides, v_pool_dev, pool_strides, nullptr,
+                        16 * max_tiles, batch, kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev,
+                        workspace_bytes, out_dev, out_strides, nullptr, batch > 1, stream, &p);
 }
 
 }  // extern "C"

@@ -196,6 +196,43 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
   }
 }
 
+// Paged cache prune: the kept suffix's keys re-rotated in place in their
+// pages. Each tile entry is {page, first slot, rows (<= 16), 0}, the format
+// of the paged decode's tile table; entries outside the pool or past a page's
+// end are skipped. A work-group covers two tiles of one (layer, head): thread
+// (tile half, row, 16-byte chunk u), which loads, rotates and stores its own
+// chunks, so the in-place update needs no ordering between threads.
+struct PagedRotateArgs {
+  uint16_t* k[kMaxJobs];  // the layers' K pools
+  float cs[kHeadDim];     // cos(angle_i) for i < 64, then sin(angle_i)
+  int64_t sp, sh, st;     // pool strides: page, head, token
+  const int32_t* tiles;   // [num_tiles, 4]
+  int64_t num_tiles;
+  int pages, page_tokens;
+};
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void paged_rotate_kernel(const PagedRotateArgs a) {
+  const int64_t tile = 2 * static_cast<int64_t>(blockIdx.x) + (threadIdx.x >> 7);
+  const int row = (threadIdx.x >> 3) & 15;
+  const int u = threadIdx.x & 7;
+  if (tile >= a.num_tiles) return;
+  const int4 e = *reinterpret_cast<const int4*>(a.tiles + 4 * tile);
+  if (e.x < 0 || e.x >= a.pages || e.y < 0 || e.z < 0 || e.z > 16 || e.y > a.page_tokens - e.z) return;
+  if (row >= e.z) return;
+  float cv[8], sv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cv[i] = a.cs[8 * u + i];
+    sv[i] = a.cs[kHalf + 8 * u + i];
+  }
+  uint16_t* p = a.k[blockIdx.z] + e.x * a.sp + static_cast<int64_t>(blockIdx.y) * a.sh + (e.y + row) * a.st + 8 * u;
+  uint4 lo = load16(p), hi = load16(p + kHalf);
+  rotate_pair<DT>(lo, hi, cv, sv);
+  store16(p, lo);
+  store16(p + kHalf, hi);
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
@@ -370,6 +407,45 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host, const int64
   if (rc != TC_OK) return rc;
   return launch_rows(k_src_host, v_src_host, k_dst_host, v_dst_host, num_layers, src_strides, dst_strides, batch,
                      heads, dtype, c0, a, c, rotate, false, cos_sin_host, s);
+}
+
+int tc_paged_rotate_keys(void* const* k_pools_host, int num_layers, const int64_t pool_strides[3], int num_pages,
+                         int page_tokens, const int32_t* tiles_dev, int64_t num_tiles, int kv_heads, int head_dim,
+                         int dtype, const float* cos_sin_host, void* stream) {
+  clear_error();
+  int rc = check_dims(1, kv_heads, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (num_layers < 0) return fail(TC_ERR_INVALID_ARGUMENT, "num_layers %d is negative", num_layers);
+  if (num_pages < 1 || page_tokens < 1)
+    return fail(TC_ERR_INVALID_ARGUMENT, "pool of %d pages of %d tokens", num_pages, page_tokens);
+  if ((rc = check_strides3("pool", pool_strides)) != TC_OK) return rc;
+  if (num_tiles < 0) return fail(TC_ERR_INVALID_ARGUMENT, "num_tiles %lld is negative", (long long)num_tiles);
+  if ((rc = check_ptrs("k_pools", k_pools_host, num_layers)) != TC_OK) return rc;
+  if (num_tiles == 0 || num_layers == 0) return TC_OK;
+  if (!tiles_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null tile list");
+  if (!aligned16(tiles_dev)) return fail(TC_ERR_ALIGNMENT, "tile list not 16-byte aligned");
+  if (!cos_sin_host) return fail(TC_ERR_INVALID_ARGUMENT, "cos_sin table is null");
+  const int64_t groups = ceil_div(num_tiles, 2);
+  if (groups > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many tiles (%lld)", (long long)num_tiles);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int l0 = 0; l0 < num_layers; l0 += kMaxJobs) {
+    const int nl = min(kMaxJobs, num_layers - l0);
+    PagedRotateArgs a;
+    for (int i = 0; i < kMaxJobs; ++i) a.k[i] = i < nl ? static_cast<uint16_t*>(k_pools_host[l0 + i]) : nullptr;
+    for (int i = 0; i < kHeadDim; ++i) a.cs[i] = cos_sin_host[i];
+    a.sp = pool_strides[0]; a.sh = pool_strides[1]; a.st = pool_strides[2];
+    a.tiles = tiles_dev;
+    a.num_tiles = num_tiles;
+    a.pages = num_pages;
+    a.page_tokens = page_tokens;
+    const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(kv_heads), static_cast<unsigned>(nl));
+    if (dtype == TC_DTYPE_F16)
+      hipLaunchKernelGGL((paged_rotate_kernel<TC_DTYPE_F16>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((paged_rotate_kernel<TC_DTYPE_BF16>), grid, dim3(kThreads), 0, s, a);
+    if ((rc = hip_status(hipGetLastError(), "paged rotate launch")) != TC_OK) return rc;
+  }
+  return TC_OK;
 }
 
 }  // extern "C"
