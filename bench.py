@@ -486,6 +486,84 @@ def measure_torch_reads(dev, n, reps=50):
     return out
 
 
+def measure_paged(dev, n, steps, page_tokens=64):
+    """The paged cache (threadcut_amd.paged): a 36-layer decode sweep at n tokens read
+    through the tile table, and the prune of the splice workload (Split(2048, 8668, 5668)
+    on 14336 tokens), whose device work is the kept keys' in-place rotation. Pages are
+    handed out from a shuffled free list, so neighbouring tiles sit on scattered pages."""
+    import random
+    import time
+
+    import torch
+
+    from threadcut_amd import _lib, kv, workloads
+    from threadcut_amd.paged import PagedKV, PageTable, _cut, tiles_of
+
+    def filled(tokens, seed):
+        pages = -(-tokens // page_tokens) + 4
+        cache = PagedKV(LAYERS, HKV, pages, page_tokens, device=dev)
+        random.Random(seed).shuffle(cache.table.free)
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        cache.append(0, [torch.randn((HKV, tokens, D), generator=g, device=dev).half() for _ in range(LAYERS)],
+                     [torch.randn((HKV, tokens, D), generator=g, device=dev).half() for _ in range(LAYERS)])
+        return cache
+
+    out = {"page_tokens": page_tokens}
+    cache = filled(n, 5)
+    gq = torch.Generator(device=dev)
+    gq.manual_seed(6)
+    qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+
+    def step():
+        for layer in range(LAYERS):
+            cache.decode(layer, qs[layer], D ** -0.5, out=outs[layer])
+
+    ms = time_graph(capture(step), steps, 5)
+    out[f"decode_{n}"] = {"us_per_call": round(ms * 1e3 / LAYERS, 3),
+                          "GB/s": round(LAYERS * decode_bytes(n) / (ms * 1e-3) / 1e9, 1)}
+    del cache, qs, outs
+    torch.cuda.empty_cache()
+
+    s = workloads.SPLICE_SPLIT
+    cache = filled(workloads.SPLICE_TOKENS, 7)
+    suffix = _cut(cache.table.frags[0], s.c0, s.c0 + s.c)
+    tiles = tiles_of(suffix)
+    t = torch.zeros((len(tiles), 4), dtype=torch.int32)
+    t[:, :3] = torch.tensor(tiles, dtype=torch.int32)
+    td = t.to(dev)
+    table = _lib.float_array(kv.rope_table(-s.gap, workloads.inv_freq(1e6)))
+    lib = _lib.load()
+    kp = _lib.ptr_array([p.data_ptr() for p in cache.k_pools])
+    st = _lib.i64x3(*cache.k_pools[0].stride()[:3])
+    pages = cache.k_pools[0].shape[0]
+
+    def rotate():
+        _lib.check(lib.tc_paged_rotate_keys(kp, LAYERS, st, pages, page_tokens, td.data_ptr(), len(tiles), HKV, D,
+                                            _lib.TC_DTYPE_F16, table, _lib.stream_of(dev)), "tc_paged_rotate_keys")
+
+    ms = time_graph(capture(rotate), max(5, steps // 10), 3)
+    nbytes = 2 * LAYERS * HKV * s.c * D * 2  # K of the kept suffix, read and written
+    # Host bookkeeping of one prune (fragment cut, free list, tile list), on copies of the table.
+    reps, t0 = 50, time.perf_counter()
+    for _ in range(reps):
+        pt = PageTable(pages, page_tokens)
+        pt.frags = [list(cache.table.frags[0])]
+        pt.free = list(cache.table.free)
+        suf, freed = pt.prune(0, s.a, s.c0, s.c)
+        tiles_of(suf)
+    host_us = (time.perf_counter() - t0) * 1e6 / reps
+    out["prune_splice_split"] = {
+        "split": [s.a, s.c0, s.c], "tokens": workloads.SPLICE_TOKENS, "layers": LAYERS,
+        "us_device": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "tiles": len(tiles),
+        "pages_freed": len(freed), "host_us_bookkeeping": round(host_us, 1)}
+    del cache, td
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_match(seconds=2.0):
     """Request split at a 131072-token cache: the native matcher vs the reference's numpy windows."""
     import numpy as np
@@ -525,7 +603,7 @@ def main():
     ap.add_argument("--no-splice", action="store_true")
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
-    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy", "prefill", "decode-step"],
+    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy", "prefill", "decode-step", "paged"],
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -553,6 +631,9 @@ def main():
         return
     if args.only == "prefill":
         print(json.dumps(measure_prefill(dev, args.steps, args.prefill_case)))
+        return
+    if args.only == "paged":
+        print(json.dumps(measure_paged(dev, args.n, max(20, args.steps // 4))))
         return
     if args.only == "decode-step":
         print(json.dumps(measure_decode_step(dev, args.n)))
@@ -615,6 +696,7 @@ def main():
         line["match_split"] = measure_match()
         line["prefill"] = measure_prefill(dev, args.steps)
         line["decode_step_model"] = measure_decode_step(dev, n)
+        line["paged"] = measure_paged(dev, n, max(20, args.steps // 4))
     if not args.no_splice:
         line["splice"] = bench_splice(dev, max(5, args.steps // 10), 3)
     if not args.no_cpu_baseline:
