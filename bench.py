@@ -531,7 +531,7 @@ def measure_paged(dev, n, steps, page_tokens=64):
     suffix = _cut(cache.table.frags[0], s.c0, s.c0 + s.c)
     tiles = tiles_of(suffix)
     t = torch.zeros((len(tiles), 4), dtype=torch.int32)
-    t[:, :3] = torch.tensor(tiles, dtype=torch.int32)
+    t[:, :3] = torch.from_numpy(tiles)
     td = t.to(dev)
     table = _lib.float_array(kv.rope_table(-s.gap, workloads.inv_freq(1e6)))
     lib = _lib.load()
@@ -549,7 +549,7 @@ def measure_paged(dev, n, steps, page_tokens=64):
     reps, t0 = 50, time.perf_counter()
     for _ in range(reps):
         pt = PageTable(pages, page_tokens)
-        pt.frags = [list(cache.table.frags[0])]
+        pt.frags = [cache.table.frags[0].copy()]
         pt.free = list(cache.table.free)
         suf, freed = pt.prune(0, s.a, s.c0, s.c)
         tiles_of(suf)

@@ -164,7 +164,7 @@ def test_paged_prune_matches_contiguous_splice(gpu, page_tokens, s):
         assert np.array_equal(bits(v), vb.view(np.int16)), f"V layer {layer}"
         want.append((kb, vb))
     # Exactly the pages no kept token uses went back to the free list.
-    kept = {p for p, _ in cache.table.token_slots(0)}
+    kept = set(cache.table.token_slots(0)[:, 0].tolist())
     assert set(freed) == used_before - kept
     assert len(freed) >= max(0, (s.c0 - s.a) // page_tokens - 1) + max(0, (n - s.c0 - s.c) // page_tokens - 1)
     # Decode on the pruned cache, then after more tokens are appended.

@@ -12,7 +12,7 @@ from threadcut_amd.paged import TILE, PageTable, tiles_of
 def check_table(t, model):
     used = set()
     for b in range(t.batch):
-        slots = t.token_slots(b)
+        slots = [tuple(x) for x in t.token_slots(b).tolist()]
         assert slots == model[b]
         assert t.length(b) == len(model[b])
         for page, slot in slots:
@@ -25,10 +25,10 @@ def check_table(t, model):
     assert len(t.free) == len(set(t.free))
     tab, cnt = t.tile_table()
     for b in range(t.batch):
-        ts = tiles_of(t.frags[b])
+        ts = tiles_of(t.frags[b]).tolist()
         assert cnt[b] == len(ts)
         rows = []
-        for (page, slot, n), e in zip(ts, tab[b]):
+        for (page, slot, n), e in zip(ts, tab[b].tolist()):
             assert tuple(e) == (page, slot, n, 0)
             assert 1 <= n <= TILE and slot + n <= t.page_tokens
             assert slot // TILE == (slot + n - 1) // TILE  # a tile never crosses a 16-slot boundary
@@ -51,7 +51,7 @@ def test_page_table_matches_brute_force(page_tokens, seed):
                 continue
             got = t.reserve(b, n)
             assert len(got) == n
-            model[b] += got
+            model[b] += [tuple(x) for x in got.tolist()]
         else:
             length = len(model[b])
             a = rnd.randint(0, length)
@@ -59,7 +59,7 @@ def test_page_table_matches_brute_force(page_tokens, seed):
             c = rnd.randint(0, length - c0)
             suffix, freed = t.prune(b, a, c0, c)
             want_suffix = model[b][c0:c0 + c]
-            assert [(p, s + i) for p, s, n in suffix for i in range(n)] == want_suffix
+            assert [(p, s + i) for p, s, n in suffix.tolist() for i in range(n)] == want_suffix
             model[b] = model[b][:a] + want_suffix
             assert all(p not in {q for q, _ in model[b]} for p in freed)
         check_table(t, model)
@@ -75,15 +75,15 @@ def test_prune_frees_whole_pages_of_the_span():
     t.reserve(0, 160)  # pages 0..9
     suffix, freed = t.prune(0, 20, 100, 60)  # keep [0,20) and [100,160)
     assert freed == [2, 3, 4, 5]  # tokens 32..95 only
-    assert suffix == [(6, 4, 12), (7, 0, 16), (8, 0, 16), (9, 0, 16)]
-    assert t.frags[0] == [(0, 0, 16), (1, 0, 4)] + suffix
+    assert suffix.tolist() == [[6, 4, 12], [7, 0, 16], [8, 0, 16], [9, 0, 16]]
+    assert t.frags[0].tolist() == [[0, 0, 16], [1, 0, 4]] + suffix.tolist()
     # The last page is full, so the next token takes a page the prune freed.
-    assert t.reserve(0, 1) == [(2, 0)]
+    assert t.reserve(0, 1).tolist() == [[2, 0]]
     t2 = PageTable(num_pages=4, page_tokens=16)
     t2.reserve(0, 20)
     t2.prune(0, 3, 10, 10)  # one page keeps both sides of the hole
-    assert t2.frags[0] == [(0, 0, 3), (0, 10, 6), (1, 0, 4)]
-    assert t2.reserve(0, 2) == [(1, 4), (1, 5)]
+    assert t2.frags[0].tolist() == [[0, 0, 3], [0, 10, 6], [1, 0, 4]]
+    assert t2.reserve(0, 2).tolist() == [[1, 4], [1, 5]]
 
 
 def test_reserve_and_prune_reject_bad_requests():

@@ -34,34 +34,52 @@ from .kv import rope_table
 TILE = 16  # rows per tile-table entry (the decode kernel's tile)
 
 
+_EMPTY = np.zeros((0, 3), dtype=np.int64)
+
+
 def _cut(frags, lo, hi):
-    """The fragments covering logical tokens [lo, hi) of a fragment list."""
-    out, pos = [], 0
-    for page, start, count in frags:
-        a, b = max(lo, pos), min(hi, pos + count)
-        if a < b:
-            out.append((page, start + a - pos, b - a))
-        pos += count
-        if pos >= hi:
-            break
-    return out
+    """The fragments (rows of an int64 [F, 3] array) covering logical tokens [lo, hi)."""
+    if hi <= lo or len(frags) == 0:
+        return _EMPTY
+    ends = np.cumsum(frags[:, 2])
+    begins = ends - frags[:, 2]
+    i0 = int(np.searchsorted(ends, lo, side="right"))
+    i1 = int(np.searchsorted(begins, hi, side="left"))
+    sub = frags[i0:i1].copy()
+    if len(sub):
+        skip = lo - begins[i0]
+        if skip > 0:
+            sub[0, 1] += skip
+            sub[0, 2] -= skip
+        over = ends[i1 - 1] - hi
+        if over > 0:
+            sub[-1, 2] -= over
+        sub = sub[sub[:, 2] > 0]
+    return sub
 
 
 def tiles_of(frags):
-    """Tile entries (page, first slot, rows) of a fragment list: each fragment
-    is cut at multiples of 16 slots, so full tiles are 16-slot aligned."""
-    out = []
-    for page, start, count in frags:
-        s, end = start, start + count
-        while s < end:
-            e = min(end, (s // TILE + 1) * TILE)
-            out.append((page, s, e - s))
-            s = e
-    return out
+    """Tile entries (page, first slot, rows) of a fragment array, int32 [T, 3]:
+    each fragment is cut at multiples of 16 slots, so full tiles are 16-slot
+    aligned."""
+    frags = np.asarray(frags, dtype=np.int64).reshape(-1, 3)
+    if len(frags) == 0:
+        return np.zeros((0, 3), dtype=np.int32)
+    start, end = frags[:, 1], frags[:, 1] + frags[:, 2]
+    t0 = start // TILE
+    nt = (end - 1) // TILE + 1 - t0
+    rep = np.repeat(np.arange(len(frags)), nt)
+    k = np.arange(int(nt.sum())) - np.repeat(np.cumsum(nt) - nt, nt)
+    lo = np.maximum(start[rep], (t0[rep] + k) * TILE)
+    hi = np.minimum(end[rep], (t0[rep] + k + 1) * TILE)
+    return np.stack([frags[rep, 0], lo, hi - lo], axis=1).astype(np.int32)
 
 
 class PageTable:
-    """Pages of `page_tokens` slots shared by `batch` sequences (host bookkeeping)."""
+    """Pages of `page_tokens` slots shared by `batch` sequences (host bookkeeping).
+
+    frags[b] is sequence b's int64 [F, 3] array of (page, first slot, count).
+    """
 
     def __init__(self, num_pages, page_tokens, batch=1):
         if num_pages < 1 or page_tokens < 1 or batch < 1:
@@ -69,7 +87,7 @@ class PageTable:
         self.num_pages = int(num_pages)
         self.page_tokens = int(page_tokens)
         self.free = list(range(self.num_pages - 1, -1, -1))  # pop() hands out the lowest id first
-        self.frags = [[] for _ in range(batch)]
+        self.frags = [_EMPTY.copy() for _ in range(batch)]
         self.version = 0  # bumped on every change, so device copies know when to refresh
 
     @property
@@ -77,66 +95,73 @@ class PageTable:
         return len(self.frags)
 
     def length(self, b):
-        return sum(c for _, _, c in self.frags[b])
+        return int(self.frags[b][:, 2].sum())
 
     def reserve(self, b, n):
-        """Slots (page, slot) for the next n tokens of sequence b, in order."""
+        """Slots of the next n tokens of sequence b, in order: int64 [n, 2] of (page, slot)."""
         if n < 0:
             raise ValueError("reserve: n must be >= 0")
+        P = self.page_tokens
         fr = self.frags[b]
-        need_pages = 0
-        room = 0
-        if fr:
-            page, start, count = fr[-1]
-            room = self.page_tokens - (start + count)
-        if n > room:
-            need_pages = -(-(n - room) // self.page_tokens)
-        if need_pages > len(self.free):
-            raise RuntimeError(f"PageTable: {need_pages} pages needed, {len(self.free)} free")
-        out = []
-        while len(out) < n:
-            if fr and fr[-1][1] + fr[-1][2] < self.page_tokens:
-                page, start, count = fr[-1]
-                take = min(n - len(out), self.page_tokens - (start + count))
-                out += [(page, start + count + i) for i in range(take)]
-                fr[-1] = (page, start, count + take)
-            else:
-                fr.append((self.free.pop(), 0, 0))
+        room = int(P - fr[-1, 1] - fr[-1, 2]) if len(fr) else 0
+        take = min(n, room)
+        rest = n - take
+        k = -(-rest // P)
+        if k > len(self.free):
+            raise RuntimeError(f"PageTable: {k} pages needed, {len(self.free)} free")
+        parts = []
+        if take:
+            page, end = int(fr[-1, 0]), int(fr[-1, 1] + fr[-1, 2])
+            parts.append(np.stack([np.full(take, page), np.arange(end, end + take)], axis=1))
+            fr = fr.copy()
+            fr[-1, 2] += take
+        if k:
+            pages = np.array([self.free.pop() for _ in range(k)], dtype=np.int64)
+            counts = np.full(k, P, dtype=np.int64)
+            counts[-1] = rest - (k - 1) * P
+            fr = np.concatenate([fr, np.stack([pages, np.zeros(k, dtype=np.int64), counts], axis=1)])
+            idx = np.arange(rest)
+            parts.append(np.stack([pages[idx // P], idx % P], axis=1))
+        self.frags[b] = fr
         self.version += 1
-        return out
+        return np.concatenate(parts).astype(np.int64) if parts else np.zeros((0, 2), dtype=np.int64)
 
     def prune(self, b, a, c0, c):
         """Keep tokens [0, a) and [c0, c0 + c) of sequence b; returns (the kept
         suffix's fragments, the pages freed)."""
+        old = self.frags[b]
         n = self.length(b)
         if not (0 <= a <= c0 and c >= 0 and c0 + c <= n):
             raise ValueError(f"prune: split (a={a}, c0={c0}, c={c}) outside a sequence of {n} tokens")
-        old = self.frags[b]
         suffix = _cut(old, c0, c0 + c)
-        new = _cut(old, 0, a) + suffix
-        # Adjacent pieces of one page merge back (a == c0 leaves the list as it was).
-        merged = []
-        for f in new:
-            if merged and merged[-1][0] == f[0] and merged[-1][1] + merged[-1][2] == f[1]:
-                merged[-1] = (f[0], merged[-1][1], merged[-1][2] + f[2])
-            else:
-                merged.append(f)
-        kept = {p for p, _, _ in merged}
-        freed = sorted({p for p, _, _ in old} - kept)
-        self.frags[b] = merged
-        self.free += sorted(freed, reverse=True)
+        head = _cut(old, 0, a)
+        if len(head) and len(suffix) and head[-1, 0] == suffix[0, 0] and head[-1, 1] + head[-1, 2] == suffix[0, 1]:
+            # Adjacent pieces of one page merge back (a == c0 leaves the list as it was).
+            joint = head[-1:].copy()
+            joint[0, 2] += suffix[0, 2]
+            new = np.concatenate([head[:-1], joint, suffix[1:]])
+        else:
+            new = np.concatenate([head, suffix])
+        freed = sorted(set(old[:, 0].tolist()) - set(new[:, 0].tolist()))
+        self.frags[b] = new
+        self.free += freed[::-1]
         self.version += 1
         return suffix, freed
 
     def release(self, b):
         """Drop sequence b entirely (its pages return to the free list)."""
-        self.free += sorted({p for p, _, _ in self.frags[b]}, reverse=True)
-        self.frags[b] = []
+        self.free += sorted(set(self.frags[b][:, 0].tolist()), reverse=True)
+        self.frags[b] = _EMPTY.copy()
         self.version += 1
 
     def token_slots(self, b):
-        """(page, slot) of every token of sequence b in logical order."""
-        return [(p, s + i) for p, s, c in self.frags[b] for i in range(c)]
+        """(page, slot) of every token of sequence b in logical order, int64 [n, 2]."""
+        fr = self.frags[b]
+        if len(fr) == 0:
+            return np.zeros((0, 2), dtype=np.int64)
+        rep = np.repeat(np.arange(len(fr)), fr[:, 2])
+        i = np.arange(len(rep)) - np.repeat(np.cumsum(fr[:, 2]) - fr[:, 2], fr[:, 2])
+        return np.stack([fr[rep, 0], fr[rep, 1] + i], axis=1)
 
     def tile_table(self):
         """int32 [B, max_tiles, 4] and tiles int32 [B] (numpy)."""
@@ -145,8 +170,7 @@ class PageTable:
         tab = np.zeros((self.batch, mt, 4), dtype=np.int32)
         cnt = np.zeros(self.batch, dtype=np.int32)
         for b, ts in enumerate(per):
-            if ts:
-                tab[b, :len(ts), :3] = np.asarray(ts, dtype=np.int32)
+            tab[b, :len(ts), :3] = ts
             cnt[b] = len(ts)
         return tab, cnt
 
@@ -193,7 +217,7 @@ class PagedKV:
         slots = self.table.reserve(b, n)
         if n == 0:
             return
-        idx = torch.tensor(slots, dtype=torch.long).to(self.device)
+        idx = torch.from_numpy(slots).to(self.device)
         pages, sl = idx[:, 0], idx[:, 1]
         for kp, vp, k, v in zip(self.k_pools, self.v_pools, ks, vs):
             k = k.reshape(self.kv_heads, n, HEAD_DIM)
@@ -204,10 +228,10 @@ class PagedKV:
     def gather(self, layer, b=0):
         """Sequence b's K and V of one layer in logical order, [Hkv, n, D] copies."""
         slots = self.table.token_slots(b)
-        if not slots:
+        if len(slots) == 0:
             z = torch.empty(self.kv_heads, 0, HEAD_DIM, dtype=self.dtype, device=self.device)
             return z, z.clone()
-        idx = torch.tensor(slots, dtype=torch.long).to(self.device)
+        idx = torch.from_numpy(slots).to(self.device)
         k = self.k_pools[layer][idx[:, 0], :, idx[:, 1]].transpose(0, 1).contiguous()
         v = self.v_pools[layer][idx[:, 0], :, idx[:, 1]].transpose(0, 1).contiguous()
         return k, v
@@ -258,9 +282,9 @@ class PagedKV:
         suffix, freed = self.table.prune(b, s.a, s.c0, s.c)
         gap = s.c0 - s.a
         tiles = tiles_of(suffix)
-        if gap and tiles:
+        if gap and len(tiles):
             t = np.zeros((len(tiles), 4), dtype=np.int32)
-            t[:, :3] = np.asarray(tiles, dtype=np.int32)
+            t[:, :3] = tiles
             td = torch.from_numpy(t).to(self.device)
             table = _lib.float_array(rope_table(-gap, inv_freq))
             lib = _lib.load()
