@@ -98,3 +98,14 @@ def test_reserve_and_prune_reject_bad_requests():
         t.prune(0, 2, 5, 6)
     tab, cnt = PageTable(3, 16, batch=2).tile_table()
     assert tab.shape == (2, 1, 4) and not tab.any() and list(cnt) == [0, 0]
+
+
+def test_paged_cache_rejects_host_pools():
+    import torch
+
+    from threadcut_amd.paged import PagedKV
+
+    with pytest.raises(RuntimeError, match="GPU"):
+        PagedKV(2, 8, 10, 16, device="cpu")
+    with pytest.raises(TypeError):
+        PagedKV(2, 8, 10, 16, dtype=torch.float32, device="cuda")

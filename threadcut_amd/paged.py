@@ -214,6 +214,9 @@ class PagedKV:
         if len(ks) != self.layers or len(vs) != self.layers:
             raise ValueError(f"append: {self.layers} layers of K and V expected")
         n = ks[0].shape[-2]
+        for t in list(ks) + list(vs):
+            if t.shape[-2] != n or t.numel() != self.kv_heads * n * HEAD_DIM:
+                raise ValueError(f"append: every layer's K and V must be [{self.kv_heads}, {n}, {HEAD_DIM}]")
         slots = self.table.reserve(b, n)
         if n == 0:
             return
@@ -257,8 +260,14 @@ class PagedKV:
             raise ValueError(f"PagedKV.decode: q {tuple(q.shape)} {q.dtype} does not fit the cache")
         if q.stride(3) != 1:
             raise ValueError("PagedKV.decode: q must have a contiguous last dimension")
+        if q.device != self.device:
+            raise ValueError(f"PagedKV.decode: q is on {q.device}, the pools on {self.device}")
+        if not 0 <= layer < self.layers:
+            raise IndexError(f"PagedKV.decode: layer {layer} outside [0, {self.layers})")
         if out is None:
             out = torch.empty_like(q)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or out.stride(3) != 1:
+            raise ValueError("PagedKV.decode: out must match q in shape, dtype and device")
         tab, cnt, mt = self.device_table()
         lib = _lib.load()
         kp, vp = self.k_pools[layer], self.v_pools[layer]
