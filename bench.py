@@ -523,7 +523,41 @@ def measure_paged(dev, n, steps, page_tokens=64):
     ms = time_graph(capture(step), steps, 5)
     out[f"decode_{n}"] = {"us_per_call": round(ms * 1e3 / LAYERS, 3),
                           "GB/s": round(LAYERS * decode_bytes(n) / (ms * 1e-3) / 1e9, 1)}
-    del cache, qs, outs
+
+    # One decode step with the new token's K/V: written into its reserved slot by
+    # two torch row copies per layer and then attended, against the fused call.
+    cache.reserve_step()
+    page, slot = (int(x) for x in cache.table.token_slots(0)[-1])
+    tab, cnt, mt = cache.device_table()
+    kns = [torch.randn((1, HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    vns = [torch.randn((1, HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    lib = _lib.load()
+    S = lib.tc_decode_num_splits(1, HKV, 16 * mt, 0, 0)
+    ws = torch.empty(lib.tc_decode_workspace_bytes(1, HKV, HQ // HKV, D, S), dtype=torch.uint8, device=dev)
+    pst = _lib.i64x3(*cache.k_pools[0].stride()[:3])
+    nst = _lib.i64x2(HKV * D, D)
+
+    def write_then_attend():
+        for layer in range(LAYERS):
+            cache.k_pools[layer][page, :, slot] = kns[layer][0]
+            cache.v_pools[layer][page, :, slot] = vns[layer][0]
+            cache.decode(layer, qs[layer], D ** -0.5, out=outs[layer])
+
+    def fused():
+        for layer in range(LAYERS):
+            kp, vp = cache.k_pools[layer], cache.v_pools[layer]
+            _lib.check(lib.tc_decode_paged_append_attention(
+                qs[layer].data_ptr(), _lib.i64x3(*qs[layer].stride()[:3]), kp.data_ptr(), vp.data_ptr(), pst,
+                kp.shape[0], kp.shape[2], tab.data_ptr(), cnt.data_ptr(), mt, kns[layer].data_ptr(), nst,
+                vns[layer].data_ptr(), nst, 1, HKV, HQ // HKV, D, _lib.TC_DTYPE_F16, D ** -0.5, 0, ws.data_ptr(),
+                ws.numel(), outs[layer].data_ptr(), _lib.i64x3(*outs[layer].stride()[:3]), _lib.stream_of(dev)),
+                "tc_decode_paged_append_attention")
+
+    ms_plain = time_graph(capture(write_then_attend), steps, 5)
+    ms_fused = time_graph(capture(fused), steps, 5)
+    out["append_step"] = {"kv_tokens": n + 1, "us_per_layer_write_then_attend": round(ms_plain * 1e3 / LAYERS, 3),
+                          "us_per_layer_fused_append": round(ms_fused * 1e3 / LAYERS, 3)}
+    del cache, qs, outs, ws
     torch.cuda.empty_cache()
 
     s = workloads.SPLICE_SPLIT

@@ -186,6 +186,28 @@ int tc_decode_paged_attention(const void* q_dev, const int64_t q_strides[3],
                               void* workspace_dev, size_t workspace_bytes,
                               void* out_dev, const int64_t out_strides[3], void* stream);
 
+/* One paged decode step with the cache append fused in, the paged form of
+ * tc_decode_append_attention. The caller has already reserved each
+ * sequence's slot for the new token, so the tile table includes it as the
+ * last row of the sequence's last tile (tiles_dev[b] >= 1). The query attends
+ * the other keys of the table from the pools and the new token straight from
+ * k_new / v_new ([B, Hkv, D], element strides (batch, head)); wave 0 of split
+ * 0 writes the new K/V row into its slot, which no other wave reads. A last
+ * tile entry that is out of range writes nothing. Workspace as
+ * tc_decode_paged_attention. This replaces GrowingLayer.update's two copies
+ * per layer (threadcut/kv.py:68-77) with the decode call for a paged cache;
+ * the reference has no counterpart. */
+int tc_decode_paged_append_attention(const void* q_dev, const int64_t q_strides[3],
+                                     void* k_pool_dev, void* v_pool_dev,
+                                     const int64_t pool_strides[3], int num_pages, int page_tokens,
+                                     const int32_t* tile_table_dev, const int32_t* tiles_dev,
+                                     int64_t max_tiles, const void* k_new_dev,
+                                     const int64_t k_new_strides[2], const void* v_new_dev,
+                                     const int64_t v_new_strides[2], int batch, int kv_heads,
+                                     int group, int head_dim, int dtype, float scale,
+                                     int split_tokens, void* workspace_dev, size_t workspace_bytes,
+                                     void* out_dev, const int64_t out_strides[3], void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* RoPE delta-shift and suffix splice                                        */
 /*                                                                           */

@@ -53,6 +53,8 @@ SIGNATURES = {
                                            _I, _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_decode_paged_attention": (_I, [_P, _I64P, _P, _P, _I64P, _I, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
                                        _P, _S, _P, _I64P, _P]),
+    "tc_decode_paged_append_attention": (_I, [_P, _I64P, _P, _P, _I64P, _I, _I, _P, _P, _I64, _P, _I64P, _P,
+                                              _I64P, _I, _I, _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_shift_keys": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I64, _I, _I, _FP, _P]),
     "tc_splice_rope": (_I, [_PP, _PP, _I, _I64P, _I, _I, _I64, _I, _I, _I64, _I64, _I64, _FP, _P]),
     "tc_splice_copy": (_I, [_PP, _PP, _I64P, _I64, _PP, _PP, _I64P, _I, _I, _I, _I, _I, _I64, _I64, _I64,

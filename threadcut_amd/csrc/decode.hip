@@ -262,10 +262,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   const int32_t len_cap = a.k_new ? nt - 1 : nt;
   int32_t len = len_cap;
   const int32_t* tab = nullptr;
+  int32_t last_tile = -1;  // paged append: the tile whose last row is the new token's slot
   if constexpr (PAGED) {
     // Token index space of 16 per tile; a tile's own row count masks the rest.
-    len = 16 * min(max(a.tiles[b], 0), static_cast<int32_t>(a.max_tiles));
+    const int32_t ntiles = min(max(a.tiles[b], 0), static_cast<int32_t>(a.max_tiles));
+    len = 16 * ntiles;
     tab = a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4;
+    if (a.k_new) last_tile = ntiles - 1;
   } else if (a.lens) {
     len = min(max(a.lens[b], 0), len_cap);
   }
@@ -296,7 +299,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     const int32_t ti = tok + lane * tok_step;
     if (ti < end) {
       const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (ti >> 4));
-      e_page = e.x; e_slot = e.y; e_rows = e.z;
+      e_page = e.x; e_slot = e.y;
+      e_rows = (ti >> 4) == last_tile ? e.z - 1 : e.z;  // the new token is attended from k_new
     }
   }
   int32_t li = 0;  // the wave's tiles loaded so far
@@ -311,7 +315,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
         const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (t0 >> 4));
         page = __builtin_amdgcn_readfirstlane(e.x);
         slot = __builtin_amdgcn_readfirstlane(e.y);
-        rows = __builtin_amdgcn_readfirstlane(e.z);
+        rows = __builtin_amdgcn_readfirstlane((t0 >> 4) == last_tile ? e.z - 1 : e.z);
       }
       ++li;
       load_paged_tile(tl, kslab, vslab, row_k, row_v, a.sk_b * 2, a.sv_b * 2, a.pages, a.page_tokens, page, slot,
@@ -425,9 +429,22 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       const bool is_v = lane >= 16;
       const int chunk = 8 * (lane & 15);
       const uint16_t* src = is_v ? a.v_new + b * a.svn_b + h * a.svn_h : a.k_new + b * a.skn_b + h * a.skn_h;
-      uint16_t* dst = is_v ? a.v_w + b * a.sv_b + h * a.sv_h + len * a.sv_t
-                           : a.k_w + b * a.sk_b + h * a.sk_h + len * a.sk_t;
-      *reinterpret_cast<uint4*>(dst + chunk) = *reinterpret_cast<const uint4*>(src + chunk);
+      uint16_t* dst = nullptr;
+      if constexpr (PAGED) {
+        // The new token's slot is the last row of the sequence's last tile;
+        // an invalid entry (or no tile) writes nothing.
+        if (last_tile >= 0) {
+          const int4 e = *reinterpret_cast<const int4*>(tab + 4 * last_tile);
+          if (!(e.x < 0 || e.x >= a.pages || e.y < 0 || e.z < 1 || e.z > 16 || e.y > a.page_tokens - e.z)) {
+            const int64_t slot = e.y + e.z - 1;
+            dst = is_v ? a.v_w + e.x * a.sv_b + h * a.sv_h + slot * a.sv_t
+                       : a.k_w + e.x * a.sk_b + h * a.sk_h + slot * a.sk_t;
+          }
+        }
+      } else {
+        dst = is_v ? a.v_w + b * a.sv_b + h * a.sv_h + len * a.sv_t : a.k_w + b * a.sk_b + h * a.sk_h + len * a.sk_t;
+      }
+      if (dst) *reinterpret_cast<uint4*>(dst + chunk) = *reinterpret_cast<const uint4*>(src + chunk);
     }
   }
 
@@ -947,6 +964,37 @@ int tc_decode_paged_attention(const void* q_dev, const int64_t q_strides[3], con
   return attention_impl(q_dev, q_strides, k_pool_dev, pool_strides, v_pool_dev, pool_strides, nullptr,
                         16 * max_tiles, batch, kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev,
                         workspace_bytes, out_dev, out_strides, nullptr, batch > 1, stream, &p);
+}
+
+int tc_decode_paged_append_attention(const void* q_dev, const int64_t q_strides[3], void* k_pool_dev,
+                                     void* v_pool_dev, const int64_t pool_strides[3], int num_pages,
+                                     int page_tokens, const int32_t* tile_table_dev, const int32_t* tiles_dev,
+                                     int64_t max_tiles, const void* k_new_dev, const int64_t k_new_strides[2],
+                                     const void* v_new_dev, const int64_t v_new_strides[2], int batch,
+                                     int kv_heads, int group, int head_dim, int dtype, float scale,
+                                     int split_tokens, void* workspace_dev, size_t workspace_bytes, void* out_dev,
+                                     const int64_t out_strides[3], void* stream) {
+  clear_error();
+  if (num_pages < 1 || page_tokens < 1)
+    return fail(TC_ERR_INVALID_ARGUMENT, "pool of %d pages of %d tokens", num_pages, page_tokens);
+  if (max_tiles < 1 || max_tiles > kMaxTokens / 16)
+    return fail(TC_ERR_INVALID_ARGUMENT, "append needs max_tiles in [1, %lld] (got %lld)",
+                (long long)(kMaxTokens / 16), (long long)max_tiles);
+  if (!tile_table_dev || !tiles_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null tile table");
+  if (!aligned16(tile_table_dev)) return fail(TC_ERR_ALIGNMENT, "tile table not 16-byte aligned");
+  if (!pool_strides) return fail(TC_ERR_INVALID_ARGUMENT, "null pool strides");
+  if (!k_new_dev || !v_new_dev || !k_new_strides || !v_new_strides)
+    return fail(TC_ERR_INVALID_ARGUMENT, "null new-token K/V");
+  if (!aligned16(k_new_dev) || !aligned16(v_new_dev))
+    return fail(TC_ERR_ALIGNMENT, "new-token K/V not 16-byte aligned");
+  for (int i = 0; i < 2; ++i)
+    if (k_new_strides[i] < 0 || v_new_strides[i] < 0 || k_new_strides[i] % 8 || v_new_strides[i] % 8)
+      return fail(TC_ERR_ALIGNMENT, "new-token K/V strides must be non-negative multiples of 8");
+  const Append app{k_new_dev, k_new_strides, v_new_dev, v_new_strides, k_pool_dev, v_pool_dev};
+  const Paged p{tile_table_dev, tiles_dev, max_tiles, num_pages, page_tokens};
+  return attention_impl(q_dev, q_strides, k_pool_dev, pool_strides, v_pool_dev, pool_strides, nullptr,
+                        16 * max_tiles, batch, kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev,
+                        workspace_bytes, out_dev, out_strides, &app, batch > 1, stream, &p);
 }
 
 }  // extern "C"

@@ -283,6 +283,59 @@ class PagedKV:
             _lib.check(rc, "tc_decode_paged_attention")
         return out
 
+    def reserve_step(self):
+        """Reserve one slot per sequence for the next decode token (once per step,
+        before layer 0); every layer's `decode_append` of that step then writes
+        its new K/V row there."""
+        for b in range(self.table.batch):
+            self.table.reserve(b, 1)
+        self._step = (self.table.version, set(range(self.layers)))
+
+    def decode_append(self, layer, q, k_new, v_new, scale, out=None, split=None):
+        """One decode step of one layer with the append fused in: k_new/v_new
+        [B, Hkv, D] (or [B, Hkv, 1, D]) go to the slots `reserve_step` took, and q
+        attends every key of its sequence including the new one. Returns out
+        [B, Hkv, G, D]."""
+        _lib.require_gpu(q, k_new, v_new, what="PagedKV.decode_append")
+        b, hkv, g, d = q.shape
+        if b != self.table.batch or hkv != self.kv_heads or d != HEAD_DIM or q.dtype != self.dtype:
+            raise ValueError(f"PagedKV.decode_append: q {tuple(q.shape)} {q.dtype} does not fit the cache")
+        if not 0 <= layer < self.layers:
+            raise IndexError(f"PagedKV.decode_append: layer {layer} outside [0, {self.layers})")
+        kn = k_new.reshape(b, hkv, HEAD_DIM) if k_new.dim() == 4 else k_new
+        vn = v_new.reshape(b, hkv, HEAD_DIM) if v_new.dim() == 4 else v_new
+        for name, t in (("q", q), ("k_new", kn), ("v_new", vn)):
+            if t.stride(-1) != 1 or t.dtype != self.dtype or t.device != self.device:
+                raise ValueError(f"PagedKV.decode_append: {name} must be {self.dtype} on {self.device}, "
+                                 "last dim contiguous")
+        if kn.shape != (b, hkv, HEAD_DIM) or vn.shape != (b, hkv, HEAD_DIM):
+            raise ValueError("PagedKV.decode_append: k_new/v_new must be [B, Hkv, D]")
+        step = getattr(self, "_step", None)
+        if step is None or step[0] != self.table.version or layer not in step[1]:
+            raise RuntimeError(f"PagedKV.decode_append: layer {layer} has no reserved slot in this step "
+                               "(call reserve_step() once per step, then each layer once)")
+        if out is None:
+            out = torch.empty_like(q)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or out.stride(3) != 1:
+            raise ValueError("PagedKV.decode_append: out must match q in shape, dtype and device")
+        tab, cnt, mt = self.device_table()
+        lib = _lib.load()
+        kp, vp = self.k_pools[layer], self.v_pools[layer]
+        with torch.cuda.device(q.device):
+            s = num_splits(b, hkv, TILE * mt, split, ragged=b > 1)
+            nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+            rc = lib.tc_decode_paged_append_attention(
+                q.data_ptr(), _lib.i64x3(*q.stride()[:3]), kp.data_ptr(), vp.data_ptr(), self._strides(),
+                kp.shape[0], kp.shape[2], tab.data_ptr(), cnt.data_ptr(), mt,
+                kn.data_ptr(), _lib.i64x2(kn.stride(0), kn.stride(1)), vn.data_ptr(),
+                _lib.i64x2(vn.stride(0), vn.stride(1)), b, hkv, g, d, _lib.dtype_code(self.dtype), float(scale),
+                int(split or 0), ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.i64x3(*out.stride()[:3]),
+                _lib.stream_of(q.device))
+            _lib.check(rc, "tc_decode_paged_append_attention")
+        step[1].discard(layer)
+        return out
+
     def prune(self, b, s, inv_freq):
         """Keep tokens [0, s.a) and [s.c0, s.c0 + s.c) of sequence b (a threadcut
         Split): the dropped span's pages are freed and the kept suffix's keys are
