@@ -176,7 +176,7 @@ int tc_decode_append_attention_at(const void* q_dev, const int64_t q_strides[3],
  * compaction. Workspace as tc_decode_attention(..., n_tokens =
  * 16 * max_tiles, ragged = batch > 1). This is decode_attention
  * (threadcut/flash_decode.py:57-69) over the paged KV with slot reuse that
- * threadcut/README.md:141-144 names as the next step. */
+ * the threadcut repository's README.md:141-144 names as the next step. */
 int tc_decode_paged_attention(const void* q_dev, const int64_t q_strides[3],
                               const void* k_pool_dev, const void* v_pool_dev,
                               const int64_t pool_strides[3], int num_pages, int page_tokens,
@@ -262,7 +262,7 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
  * tc_decode_paged_attention) are rotated. Entries must not overlap (a row
  * listed twice is rotated twice); invalid entries are skipped. With pages,
  * dropping the pruned span frees its pages, so this replaces the suffix move
- * of threadcut/kv.py:28-41,83-92, as threadcut/README.md:141-144 proposes. */
+ * of threadcut/kv.py:28-41,83-92, as the threadcut repository's README.md:141-144 proposes. */
 int tc_paged_rotate_keys(void* const* k_pools_host, int num_layers, const int64_t pool_strides[3],
                          int num_pages, int page_tokens, const int32_t* tiles_dev,
                          int64_t num_tiles, int kv_heads, int head_dim, int dtype,
