@@ -122,6 +122,30 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3],
                         void* workspace_dev, size_t workspace_bytes,
                         void* out_dev, const int64_t out_strides[3], void* stream);
 
+/* Bytes of the static scratch array of tc_decode_attention_noalloc (per GPU). */
+#define TC_DECODE_SCRATCH_BYTES (8u << 20)
+
+/* tc_decode_attention without a workspace. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc). The split partials go to a
+ * static device array of TC_DECODE_SCRATCH_BYTES that each GPU holds until
+ * the process ends; the only runtime call besides the two kernel launches is
+ * a lookup of that array's address at the first call on a device. A call
+ * whose plan needs more than the array (tc_decode_workspace_bytes(...) >
+ * TC_DECODE_SCRATCH_BYTES) returns TC_ERR_WORKSPACE and enqueues nothing.
+ * The tensors must be on the current device. Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, unordered host
+ * threads) race and give wrong results; calls ordered on one stream do not.
+ * Nothing in the array needs clearing: the partial pass writes every slot the
+ * combine pass reads. */
+int tc_decode_attention_noalloc(const void* q_dev, const int64_t q_strides[3],
+                                const void* k_dev, const int64_t k_strides[3],
+                                const void* v_dev, const int64_t v_strides[3],
+                                const int32_t* lens_dev, int64_t n_tokens,
+                                int batch, int kv_heads, int group, int head_dim, int dtype,
+                                float scale, int split_tokens,
+                                void* out_dev, const int64_t out_strides[3], void* stream);
+
 /* Append-and-attend for one decode step. The new token's K/V rows k_new /
  * v_new [B, Hkv, D] (element strides (batch, head), last dim contiguous) are
  * written to row n_tokens - 1 of k_cache / v_cache, and the query attends over

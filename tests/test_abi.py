@@ -32,6 +32,24 @@ def test_every_declared_symbol_is_exported(lib):
         assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
 
 
+def test_scratch_size_matches_header():
+    m = re.search(r"#define TC_DECODE_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.TC_DECODE_SCRATCH_BYTES
+
+
+def test_noalloc_refuses_plans_beyond_its_scratch(lib):
+    # 16 x 8 KV heads x 8 query heads at 64-token splits of 4096 tokens: 33 MB of partials.
+    # Refused on the host (the split length is given, so no device is queried).
+    b, h, g, d, n = 16, 8, 8, 128, 4096
+    s = lib.tc_decode_num_splits(b, h, n, 64, 0)
+    assert lib.tc_decode_workspace_bytes(b, h, g, d, s) > _lib.TC_DECODE_SCRATCH_BYTES
+    st = _lib.i64x3(h * n * d, n * d, d)
+    rc = lib.tc_decode_attention_noalloc(16, _lib.i64x3(h * g * d, g * d, d), 32, st, 48, st, None, n, b, h, g, d,
+                                         _lib.TC_DTYPE_F16, 0.088, 64, 64, _lib.i64x3(h * g * d, g * d, d), None)
+    assert rc == _lib.TC_ERR_WORKSPACE
+    assert "static scratch" in lib.tc_last_error().decode()
+
+
 def test_version_and_messages(lib):
     assert lib.tc_abi_version() == 1
     for code in range(6):

@@ -22,6 +22,7 @@ TC_ERR_HIP = 5
 TC_DTYPE_F16 = 0
 TC_DTYPE_BF16 = 1
 TC_MAX_SPLITS = 4096
+TC_DECODE_SCRATCH_BYTES = 8 << 20  # static scratch of tc_decode_attention_noalloc, per GPU
 
 _DTYPES = {torch.float16: TC_DTYPE_F16, torch.bfloat16: TC_DTYPE_BF16}
 
@@ -47,6 +48,8 @@ SIGNATURES = {
     "tc_decode_combine": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _I64P, _I, _P]),
     "tc_decode_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
                                  _P, _S, _P, _I64P, _P]),
+    "tc_decode_attention_noalloc": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
+                                         _P, _I64P, _P]),
     "tc_decode_append_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I64, _I, _I, _I,
                                         _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_decode_append_attention_at": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I,

@@ -34,6 +34,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "tc_common.hpp"
 
@@ -893,6 +894,72 @@ int tc_decode_attention(const void* q_dev, const int64_t q_strides[3], const voi
   clear_error();
   return attention_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads,
                         group, head_dim, dtype, scale, split_tokens, workspace_dev, workspace_bytes, out_dev,
+                        out_strides, nullptr, lens_dev != nullptr, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split partials of tc_decode_attention_noalloc
+// live in `scratch`, a static array that every GPU the library runs on holds
+// until the process ends. Its device address differs per GPU and is taken
+// once per device with hipGetSymbolAddress; host code never passes the
+// array's own name to a kernel.
+// ---------------------------------------------------------------------------
+
+static __device__ __align__(256) unsigned char scratch[TC_DECODE_SCRATCH_BYTES];
+
+namespace tc {
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_dev[kScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on first use).
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  int rc = hip_status(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != TC_OK) return rc;
+  if (dev < 0 || dev >= kScratchDevices) return fail(TC_ERR_HIP, "device id %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (rc != TC_OK) return rc;
+    if (!p || !aligned16(p)) return fail(TC_ERR_HIP, "scratch symbol address %p unusable", p);
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return TC_OK;
+}
+
+}  // namespace
+}  // namespace tc
+
+extern "C" {
+
+int tc_decode_attention_noalloc(const void* q_dev, const int64_t q_strides[3], const void* k_dev,
+                                const int64_t k_strides[3], const void* v_dev, const int64_t v_strides[3],
+                                const int32_t* lens_dev, int64_t n_tokens, int batch, int kv_heads, int group,
+                                int head_dim, int dtype, float scale, int split_tokens, void* out_dev,
+                                const int64_t out_strides[3], void* stream) {
+  clear_error();
+  int rc = check_common(batch, kv_heads, group, head_dim, dtype);
+  if (rc != TC_OK) return rc;
+  if (n_tokens < 0) return fail(TC_ERR_INVALID_ARGUMENT, "n_tokens %lld is negative", (long long)n_tokens);
+  int S = 0, t = 0;
+  if ((rc = split_plan(batch, kv_heads, n_tokens, split_tokens, lens_dev != nullptr, &S, &t)) != TC_OK) return rc;
+  const size_t need = tc_decode_workspace_bytes(batch, kv_heads, group, head_dim, S);
+  if (need > TC_DECODE_SCRATCH_BYTES)
+    return fail(TC_ERR_WORKSPACE,
+                "%d splits of batch %d x %d kv heads x %d query heads need %zu bytes of partials; the static scratch "
+                "holds %zu (pass a workspace to tc_decode_attention instead)",
+                S, batch, kv_heads, group, need, (size_t)TC_DECODE_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (S > 0 && (rc = scratch_on_current_device(&ws)) != TC_OK) return rc;
+  return attention_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads,
+                        group, head_dim, dtype, scale, split_tokens, ws, TC_DECODE_SCRATCH_BYTES, out_dev,
                         out_strides, nullptr, lens_dev != nullptr, stream);
 }
 
