@@ -193,10 +193,7 @@ def measure_sweep(dev, n, steps, warmup, split, only):
 
     from threadcut_amd import flash_decode, workloads
 
-    ks, vs = workloads.layer_caches(2, LAYERS, n, device=dev)
-    gq = torch.Generator(device=dev)
-    gq.manual_seed(2)
-    qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
     outs = [torch.empty_like(q) for q in qs]
     plans = [flash_decode.DecodePlan(q, k, v, D ** -0.5, o, split=split or None)
              for q, k, v, o in zip(qs, ks, vs, outs)]

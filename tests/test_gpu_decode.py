@@ -297,3 +297,39 @@ def test_append_bf16_eight_query_heads_per_kv_head(gpu):
     assert torch.equal(kc.cpu(), k_ref) and torch.equal(vc.cpu(), v_ref)
     ref = f64_ref(q, k_ref[:, :, :n], v_ref[:, :, :n])
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 4e-3
+
+
+def test_gate_sends_supported_calls_to_the_kernels(gpu, monkeypatch):
+    """fp16 and bf16 calls at head_dim 128 run the HIP kernels, never SDPA."""
+
+    def no_sdpa(*a, **k):
+        raise AssertionError("SDPA called for a call the kernels take")
+
+    monkeypatch.setattr(attention.F, "scaled_dot_product_attention", no_sdpa)
+    for dtype, tol in ((torch.float16, TOL), (torch.bfloat16, 4e-3)):
+        q, k, v, _ = workloads.decode_inputs(41, n=300, dtype=dtype)
+        print(f"case: gate {dtype} n=300", flush=True)
+        out, _ = attention.attention(None, q.to(gpu), k.to(gpu), v.to(gpu), None, scaling=SCALE)
+        torch.cuda.synchronize()
+        ref = f64_ref(q, k, v).reshape(1, 1, 32, 128)
+        assert np.abs(out.float().cpu().numpy() - ref).max() <= tol
+
+
+@pytest.mark.parametrize("dtype,d,hq,hkv", [(torch.float32, 128, 32, 8), (torch.float16, 64, 32, 8),
+                                            (torch.float16, 128, 32, 2)])
+def test_gate_keeps_the_reference_path_for_other_calls(gpu, monkeypatch, dtype, d, hq, hkv):
+    """float32, head_dim 64 and 16 query heads per KV head are not kernel shapes: the reference's
+    folded SDPA runs on the GPU tensors (threadcut/attention.py:40-42), not the kernels."""
+
+    def no_kernel(*a, **k):
+        raise AssertionError("decode kernel called for a call it does not take")
+
+    monkeypatch.setattr(attention, "decode_into", no_kernel)
+    q, k, v, _ = workloads.decode_inputs(42, n=200, q_heads=hq, kv_heads=hkv, head_dim=d, dtype=dtype)
+    print(f"case: gate {dtype} d={d} hq={hq} hkv={hkv}", flush=True)
+    out, _ = attention.attention(None, q.to(gpu), k.to(gpu), v.to(gpu), None, scaling=d ** -0.5)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == (1, 1, hq, d) and out.is_contiguous()
+    ref = od.attention_f64(q.float().numpy().reshape(1, hkv, hq // hkv, d), k.float().numpy(), v.float().numpy(),
+                           d ** -0.5).reshape(1, 1, hq, d)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= (1e-5 if dtype == torch.float32 else TOL)

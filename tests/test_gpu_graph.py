@@ -174,3 +174,35 @@ def test_decode_graph_capacity_guard(model):
         dg.step([1])
     dg.close()
     assert cache.layers[0].n == dg.capacity
+
+
+@torch.no_grad()
+def test_decode_graph_refuses_changes_outside_the_graph(model):
+    """While a DecodeGraph holds the cache, splice, crop and eager updates raise (the captured
+    kernels hold the buffers' addresses and the device position); a layer changed behind the
+    graph's back stops step(); after close() the cache splices and decodes again."""
+    dev = model.device
+    cache = kv.new_cache(model.config, fused_append=True)
+    model(input_ids=torch.tensor([ids_of(30, 15)], device=dev), past_key_values=cache, use_cache=True)
+    dg = DecodeGraph(model, cache, max_new_tokens=4)
+    dg.step([5])
+    inv = model.model.rotary_emb.inv_freq
+    with pytest.raises(RuntimeError, match="DecodeGraph holds"):
+        kv.splice(cache, kv.Split(5, 10, 20), inv)
+    with pytest.raises(RuntimeError, match="DecodeGraph holds"):
+        cache.layers[1].crop(10)
+    with pytest.raises(RuntimeError, match="DecodeGraph holds"):
+        model(input_ids=torch.tensor([[7]], device=dev), past_key_values=cache, use_cache=True)
+    assert dg.n == 31
+    dg.step([6])
+    cache.layers[2].n -= 1  # a change the graph cannot see
+    with pytest.raises(RuntimeError, match="changed outside"):
+        dg.step([7])
+    cache.layers[2].n += 1
+    dg.close()
+    with pytest.raises(RuntimeError, match="closed"):
+        dg.step([8])
+    kv.splice(cache, kv.Split(5, 10, 22), inv)
+    assert cache.get_seq_length() == 27
+    out = model(input_ids=torch.tensor([[9]], device=dev), past_key_values=cache, use_cache=True).logits
+    assert bool(torch.isfinite(out).all()) and cache.get_seq_length() == 28

@@ -240,3 +240,38 @@ def test_fused_paged_append_matches_append_then_decode(gpu, lens, P, dt):
                 assert excess.max() <= 0
     with pytest.raises(RuntimeError, match="reserve_step"):
         fused.decode_append(0, qs[0].to(gpu), kn[0].to(gpu), vn[0].to(gpu), SCALE)
+
+
+def test_decode_and_prune_refused_while_a_step_is_pending(gpu):
+    """After reserve_step() the tile table holds each sequence's unwritten slot: decode() and
+    prune() refuse until every layer has run decode_append (or cancel_step() drops the slots)."""
+    cache, host = filled(gpu, 2, [100, 40], 16, 71)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(71)
+    q = torch.randn((2, 8, 4, 128), generator=g, device=gpu).half()
+    kn = torch.randn((2, 8, 128), generator=g, device=gpu).half()
+    before = [cache.length(0), cache.length(1)]
+    cache.reserve_step()
+    assert [cache.length(0), cache.length(1)] == [101, 41]
+    with pytest.raises(RuntimeError, match="incomplete"):
+        cache.decode(0, q, SCALE)
+    with pytest.raises(RuntimeError, match="incomplete"):
+        cache.prune(0, Split(10, 20, 30), workloads.inv_freq())
+    with pytest.raises(RuntimeError, match="incomplete"):
+        cache.reserve_step()
+    cache.cancel_step()
+    assert [cache.length(0), cache.length(1)] == before
+    out = cache.decode(0, q, SCALE)  # the step is gone: the old keys decode as before
+    torch.cuda.synchronize()
+    for b in range(2):
+        k, v = host[b][0]
+        want = closed_form(q[b:b + 1].cpu(), k[None], v[None])
+        assert np.abs(out[b:b + 1].float().cpu().numpy() - want).max() <= TOL[torch.float16]
+    cache.reserve_step()
+    cache.decode_append(0, q, kn, kn, SCALE)
+    with pytest.raises(RuntimeError, match="incomplete"):
+        cache.decode(1, q, SCALE)
+    cache.decode_append(1, q, kn, kn, SCALE)
+    cache.decode(1, q, SCALE)  # the step is complete
+    cache.prune(0, Split(10, 20, 30), workloads.inv_freq())
+    assert cache.length(0) == 40

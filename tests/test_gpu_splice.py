@@ -170,11 +170,3 @@ def test_bf16_splice(gpu, s):
         kb, vb, _ = oracle_splice(ks[i], vs[i], s, inv, dtype="bfloat16")
         assert np.array_equal(bits(layer.kbuf[:, :, :2000]), bits(kb))
         assert np.array_equal(bits(layer.vbuf[:, :, :2000]), bits(vb))
-
-
-def test_rejects_cpu_tensors():
-    layer = kv.GrowingLayer()
-    k = torch.randn(1, 8, 20, 128).half()
-    layer.update(k, k)
-    with pytest.raises(RuntimeError, match="GPU"):
-        layer.splice(Split(2, 5, 10), workloads.inv_freq())

@@ -121,20 +121,27 @@ def test_new_cache_has_growing_layers():
     assert len(cache.layers) == 3 and all(isinstance(layer, kv.GrowingLayer) for layer in cache.layers)
 
 
-def test_hot_path_refuses_host_tensors():
+def test_kernel_entry_points_refuse_host_tensors():
+    """The kernel wrappers (the reference's decode_attention is a GPU kernel too) refuse host
+    tensors; the attention interface, shift_keys and splice run the reference's torch path for
+    them instead (tests/test_cpu_path.py)."""
     q, k, v, _ = workloads.decode_inputs(0, n=32)
     with pytest.raises(RuntimeError, match="GPU"):
         flash_decode.decode_attention(q.reshape(8, 4, 128), k[0], v[0], 0.1)
     with pytest.raises(RuntimeError, match="GPU"):
-        attention.attention(None, q, k, v, None)
-    with pytest.raises(RuntimeError, match="GPU"):
-        kv.shift_keys(k, -3, workloads.inv_freq())
+        flash_decode.decode_attention_batched(q.reshape(1, 8, 4, 128), k, v, 0.1)
     layer = kv.GrowingLayer()
     layer.update(k, v)
-    with pytest.raises(RuntimeError, match="GPU"):
-        layer.splice(Split(2, 5, 10), workloads.inv_freq())
     with pytest.raises(ValueError, match="past"):
         layer.splice(Split(2, 25, 10), workloads.inv_freq())
+
+
+def test_decode_gate():
+    """flash_decode.supports decides from the tensors alone which decode calls the kernels take."""
+    q = torch.empty(1, 32, 1, 128, dtype=torch.float16)
+    k = torch.empty(1, 8, 10, 128, dtype=torch.float16)
+    assert not flash_decode.supports(q, k, k)  # host tensors
+    assert not flash_decode.supports(q.float(), k.float(), k.float())
 
 
 def test_prefill_branch_is_masked_sdpa():

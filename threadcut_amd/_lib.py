@@ -25,6 +25,7 @@ TC_MAX_SPLITS = 4096
 TC_DECODE_SCRATCH_BYTES = 8 << 20  # static scratch of tc_decode_attention_noalloc, per GPU
 
 _DTYPES = {torch.float16: TC_DTYPE_F16, torch.bfloat16: TC_DTYPE_BF16}
+DTYPES = tuple(_DTYPES)  # element types the kernels take
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int

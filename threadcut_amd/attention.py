@@ -4,11 +4,16 @@ Drop-in for threadcut/attention.py:22-51. Decode (one query token, no mask):
 the g query heads sharing a KV head are handed to the split-KV HIP kernels of
 ``flash_decode`` together with the unexpanded cache views, for any batch
 size (the reference used its GPU kernel for b == 1 and SDPA otherwise; both
-compute the same softmax). Prefill (threadcut/attention.py:43-46) runs the
-GQA-native HIP kernel of ``prefill`` on the unexpanded K/V for GPU tensors
-with head_dim 128, g in (1, 2, 4, 8) and no mask or a boolean [b|1, 1, q, n]
-mask (what the registered ``sdpa_mask`` produces). Other calls, host tensors
-included, keep the reference's own path: expand KV once and run SDPA.
+compute the same softmax), whenever the kernels take the tensors
+(``flash_decode.supports``: GPU, float16/bfloat16, head_dim 128, g <= 8).
+Other decode calls, host tensors included, keep the reference's own decode
+path for them (threadcut/attention.py:40-42): SDPA with each group's query
+heads folded into a length-g query against the unexpanded cache. Prefill
+(threadcut/attention.py:43-46) runs the GQA-native HIP kernel of ``prefill``
+on the unexpanded K/V for GPU tensors in float16/bfloat16 with head_dim 128,
+g in (1, 2, 4, 8) and no mask or a boolean [b|1, 1, q, n] mask (what the
+registered ``sdpa_mask`` produces). Other prefill calls keep the reference's
+own path: expand KV once and run SDPA.
 """
 import torch
 import torch.nn.functional as F
@@ -16,7 +21,7 @@ from transformers import AttentionInterface
 from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 
 from . import kv, prefill
-from .flash_decode import decode_append_at, decode_append_into, decode_into
+from .flash_decode import decode_append_at, decode_append_into, decode_into, supports as decode_supports
 
 NAME = "threadcut"
 
@@ -39,6 +44,14 @@ def attention(module, query, key, value, attention_mask, dropout=0.0, scaling=No
     hkv = key.shape[1]
     g = hq // hkv
     scaling = scaling if scaling is not None else d ** -0.5
+    if q == 1 and attention_mask is None and not decode_supports(query, key, value):
+        # The reference's decode path for calls its GPU kernel does not serve
+        # (attention.py:40-42): the g query heads of a KV head as a length-g query.
+        pending = kv.take_pending(key)
+        if pending is not None:
+            pending.flush()
+        out = F.scaled_dot_product_attention(query.reshape(b, hkv, g, d), key, value, scale=scaling)
+        return out.reshape(b, hq, 1, d).transpose(1, 2).contiguous(), None
     if q == 1 and attention_mask is None:
         # [b, 1, hq, d] contiguous is [b, hkv, g, d] with head index h*g + i.
         out = torch.empty((b, 1, hq, d), dtype=query.dtype, device=query.device)

@@ -18,6 +18,25 @@ HEAD_DIM = 128
 SPLIT_GRANULE = 64  # tokens; split lengths are rounded up to this
 
 
+def supports(query, key, value):
+    """True if the HIP decode kernels take this attention-interface call:
+    query [b, hq, 1, d], key/value [b, hkv, n, d] on one GPU, float16 or
+    bfloat16, d = 128, 1 <= hq / hkv <= 8, contiguous last dimensions.
+    Decided from the tensors alone, so a missing library still raises when a
+    supported call reaches it."""
+    b, hq, _, d = query.shape
+    hkv = key.shape[1]
+    if not (query.is_cuda and key.is_cuda and value.is_cuda):
+        return False
+    if not (query.device == key.device == value.device):
+        return False
+    if query.dtype not in _lib.DTYPES or key.dtype != query.dtype or value.dtype != query.dtype:
+        return False
+    if d != HEAD_DIM or hkv < 1 or hq % hkv or not 1 <= hq // hkv <= 8:
+        return False
+    return query.stride(-1) == 1 and key.stride(-1) == 1 and value.stride(-1) == 1
+
+
 def num_splits(batch, kv_heads, n_tokens, split=None, ragged=False):
     """KV splits a call of this size uses (``split=None``: tuned to fill the GPU)."""
     lib = _lib.load()

@@ -58,6 +58,9 @@ class DecodeGraph:
             l._reserve(n + max_new_tokens + 1, l.kbuf)
             l._view()
         self.capacity = layers[0].kbuf.shape[-2]
+        # The captured kernels hold these buffers' addresses: keep the tensors, and check
+        # before every replay that each layer still uses them.
+        self.buffers = [(l.kbuf, l.vbuf) for l in layers]
         self.pos = torch.full((batch,), n, dtype=torch.int32, device=dev)
         self.position_ids = torch.full((batch, 1), n, dtype=torch.long, device=dev)
         self.ids = torch.zeros((batch, 1), dtype=torch.long, device=dev)
@@ -84,8 +87,14 @@ class DecodeGraph:
         # One new token per sequence sees every cached token: no mask. Handing the
         # (empty) mask mapping over keeps transformers from building a mask tensor,
         # which it does while a graph is being captured.
-        out = self.model(input_ids=self.ids, position_ids=self.position_ids, past_key_values=self.cache,
-                         attention_mask={"full_attention": None}, use_cache=True, logits_to_keep=1)
+        for l in self.layers:
+            l.in_graph_step = True
+        try:
+            out = self.model(input_ids=self.ids, position_ids=self.position_ids, past_key_values=self.cache,
+                             attention_mask={"full_attention": None}, use_cache=True, logits_to_keep=1)
+        finally:
+            for l in self.layers:
+                l.in_graph_step = False
         logits = out.logits[:, -1]
         self.pos.add_(1)
         self.position_ids.add_(1)
@@ -105,8 +114,14 @@ class DecodeGraph:
 
     def step(self, ids):
         """Feed token ids [B] (or [B, 1], device or host) and return the logits [B, vocab]."""
-        if self.layers[0].n + 1 > self.capacity:
+        if self.graph is None:
+            raise RuntimeError("DecodeGraph: closed")
+        n = self.layers[0].n
+        if n + 1 > self.capacity:
             raise RuntimeError(f"DecodeGraph: the cache holds {self.capacity} tokens; close() and grow it")
+        for l, (kb, vb) in zip(self.layers, self.buffers):
+            if l.kbuf is not kb or l.vbuf is not vb or l.n != n or l.device_pos is not self.pos:
+                raise RuntimeError("DecodeGraph: the cache changed outside the graph since capture")
         self.ids.copy_(torch.as_tensor(ids).reshape(self.batch, 1), non_blocking=True)
         self.graph.replay()
         for l in self.layers:

@@ -5,7 +5,9 @@ compose, so rotating a key stored at position p by -gap gives the key at
 p - gap; values carry no position and move unchanged. The per-layer torch op
 chains of the reference (about eight kernels and fp32 temporaries per layer,
 36 layers) become one HIP launch (``tc_splice_rope``) that gathers, rotates
-and stores every layer's suffix in place.
+and stores every layer's suffix in place. Tensors the kernels do not take
+(host tensors, float32, head_dim other than 128) keep the reference's own
+torch op sequence, which is what the reference runs for them.
 
 The rotation table cos/sin(delta * inv_freq) is built on the host with the
 reference's own op order (threadcut/kv.py:22-23) and passed by value in the
@@ -62,6 +64,33 @@ def rope_table(delta, inv_freq):
     return torch.cat((emb.cos()[:half], emb.sin()[:half]))
 
 
+def _hip_ok(t):
+    """True if the HIP splice kernels take this cache tensor."""
+    return t.is_cuda and t.dtype in _lib.DTYPES and t.shape[-1] == HEAD_DIM and t.stride(-1) == 1
+
+
+def _shift_keys_torch(keys, delta, inv_freq):
+    """The reference's rotation in torch ops (threadcut/kv.py:20-25): fp32 math on the
+    keys' device, k*cos + rotate_half(k)*sin, cast back to the keys' dtype."""
+    table = rope_table(delta, inv_freq).to(keys.device)
+    half = table.numel() // 2
+    cos = torch.cat((table[:half], table[:half]))
+    sin = torch.cat((table[half:], table[half:]))
+    k = keys.float()
+    return (k * cos + rotate_half(k) * sin).to(keys.dtype)
+
+
+def _splice_layer_torch(kbuf, vbuf, s, inv_freq):
+    """GrowingLayer.splice of the reference (threadcut/kv.py:83-92) on one layer's buffers:
+    C read out (keys rotated by -gap, or copied when gap is 0), then written at a."""
+    if s.c:
+        k = kbuf[..., s.c0:s.c0 + s.c, :]
+        k = _shift_keys_torch(k, -s.gap, inv_freq) if s.gap else k.clone()
+        v = vbuf[..., s.c0:s.c0 + s.c, :].clone()
+        kbuf[..., s.a:s.a + s.c, :] = k
+        vbuf[..., s.a:s.a + s.c, :] = v
+
+
 def _as4(t):
     if t.dim() == 4:
         return t
@@ -75,10 +104,12 @@ def _as4(t):
 def shift_keys(keys, delta, inv_freq):
     """Move post-RoPE keys by `delta` positions (negative = left); new tensor.
 
-    threadcut/kv.py:20-25: fp32 math, result in keys.dtype. keys is any
-    [..., tokens, 128] fp16/bf16 GPU tensor with a contiguous last dim.
+    threadcut/kv.py:20-25: fp32 math, result in keys.dtype. A [..., tokens, 128]
+    fp16/bf16 GPU tensor with a contiguous last dim runs the HIP kernel; other
+    keys (host tensors, float32, other head dims) the reference's torch ops.
     """
-    _lib.require_gpu(keys, what="shift_keys")
+    if not _hip_ok(keys):
+        return _shift_keys_torch(keys, delta, inv_freq)
     k4 = _as4(keys)
     b, h, t, d = k4.shape
     if d != HEAD_DIM:
@@ -129,20 +160,28 @@ def splice(cache, s, inv_freq):
     if all(isinstance(layer, GrowingLayer) for layer in cache.layers):
         live = [layer for layer in cache.layers if getattr(layer, "kbuf", None) is not None]
         for layer in live:
+            layer._check_not_captured("splice")
+        for layer in live:
             layer.flush()
         for layer in live:
             if s.c0 + s.c > layer.n:
                 raise ValueError(f"splice: suffix [{s.c0}, {s.c0 + s.c}) past the {layer.n} cached tokens")
         if s.c and s.gap:
             for group in _group_by_layout(live):
-                _splice_buffers([l.kbuf for l in group], [l.vbuf for l in group], s, inv_freq)
+                if _hip_ok(group[0].kbuf):
+                    _splice_buffers([l.kbuf for l in group], [l.vbuf for l in group], s, inv_freq)
+                else:
+                    for l in group:
+                        _splice_layer_torch(l.kbuf, l.vbuf, s, inv_freq)
         for layer in live:
             layer.n = s.a + s.c
             layer._view()
         return
     layers = cache.layers
     k0 = layers[0].keys
-    _lib.require_gpu(k0, what="splice")
+    if not all(_hip_ok(t) for l in layers for t in (l.keys, l.values)):
+        _splice_index_select_torch(layers, s, inv_freq)
+        return
     b, h, n, d = k0.shape
     if s.c0 + s.c > n or s.a > n:
         raise ValueError(f"splice: split {s} past the {n} cached tokens")
@@ -169,6 +208,22 @@ def splice(cache, s, inv_freq):
         layer.keys, layer.values = k, v
 
 
+def _splice_index_select_torch(layers, s, inv_freq):
+    """The reference's splice of plain DynamicLayers (threadcut/kv.py:34-41) in torch ops:
+    keep [0, a) and [c0, c0 + c), then rotate the kept suffix's keys by -gap."""
+    n = layers[0].keys.shape[-2]
+    if s.c0 + s.c > n or s.a > n:
+        raise ValueError(f"splice: split {s} past the {n} cached tokens")
+    device = layers[0].keys.device
+    keep = torch.cat((torch.arange(0, s.a), torch.arange(s.c0, s.c0 + s.c))).to(device)
+    for layer in layers:
+        k = layer.keys.index_select(2, keep)
+        v = layer.values.index_select(2, keep)
+        if s.c and s.gap:
+            k[:, :, s.a:] = _shift_keys_torch(k[:, :, s.a:], -s.gap, inv_freq)
+        layer.keys, layer.values = k, v
+
+
 class GrowingLayer(DynamicLayer):
     """DynamicLayer backed by a preallocated buffer (threadcut/kv.py:44-92).
 
@@ -188,6 +243,15 @@ class GrowingLayer(DynamicLayer):
     # count, so the decode kernel takes the append position from the device
     # (tc_decode_append_attention_at) instead of from the host-side n.
     device_pos = None
+    # True while graph.DecodeGraph runs its own step body (warm-up, capture).
+    in_graph_step = False
+
+    def _check_not_captured(self, what):
+        """A layer held by a live DecodeGraph changes only through the graph's step:
+        anything else would leave the captured kernels writing stale positions or
+        freed buffers."""
+        if self.device_pos is not None and not self.in_graph_step:
+            raise RuntimeError(f"GrowingLayer.{what}: a DecodeGraph holds this cache; close() it first")
 
     def lazy_initialization(self, key_states, value_states):
         super().lazy_initialization(key_states, value_states)
@@ -218,6 +282,7 @@ class GrowingLayer(DynamicLayer):
         self.keys, self.values = self.kbuf[..., :self.n, :], self.vbuf[..., :self.n, :]
 
     def update(self, key_states, value_states, *args, **kwargs):
+        self._check_not_captured("update")
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
         self.flush()
@@ -234,17 +299,22 @@ class GrowingLayer(DynamicLayer):
         return self.keys, self.values
 
     def crop(self, max_length):
+        self._check_not_captured("crop")
         self.flush()
         self.n = min(self.n, max_length)
         self._view()
 
     def splice(self, s, inv_freq):
         """In-place A·B·C -> A·C: only C is touched, so a prune costs O(|C|)."""
+        self._check_not_captured("splice")
         self.flush()
         if s.c0 + s.c > self.n:
             raise ValueError(f"splice: suffix [{s.c0}, {s.c0 + s.c}) past the {self.n} cached tokens")
         if s.c and s.gap:
-            _splice_buffers([self.kbuf], [self.vbuf], s, inv_freq)
+            if _hip_ok(self.kbuf):
+                _splice_buffers([self.kbuf], [self.vbuf], s, inv_freq)
+            else:
+                _splice_layer_torch(self.kbuf, self.vbuf, s, inv_freq)
         self.n = s.a + s.c
         self._view()
 

@@ -248,12 +248,33 @@ class PagedKV:
                                tab.shape[1])
         return self._dev_table[1:]
 
+    def _step_pending(self):
+        """True between reserve_step() and the last layer's decode_append of that step:
+        the tile table then includes slots no layer has written yet."""
+        step = getattr(self, "_step", None)
+        return step is not None and step[0] == self.table.version and bool(step[1])
+
+    def _refuse_during_step(self, what):
+        if self._step_pending():
+            raise RuntimeError(f"PagedKV.{what}: a reserved decode step is incomplete; run decode_append for "
+                               "every layer (or cancel_step()) first")
+
+    def cancel_step(self):
+        """Drop the slots of an incomplete reserved step (each sequence's last token)."""
+        if not self._step_pending():
+            return
+        for b in range(self.table.batch):
+            n = self.table.length(b)
+            self.table.prune(b, n - 1, n, 0)
+        self._step = None
+
     def decode(self, layer, q, scale, out=None, split=None):
         """softmax(q·Kᵀ·scale)·V over each sequence's keys of one layer.
 
         q [B, Hkv, G, D] (G query heads per KV head, last dim contiguous) in the
         pools' dtype; returns out [B, Hkv, G, D]. Enqueued on the current stream.
         """
+        self._refuse_during_step("decode")
         _lib.require_gpu(q, what="PagedKV.decode")
         b, hkv, g, d = q.shape
         if b != self.table.batch or hkv != self.kv_heads or d != HEAD_DIM or q.dtype != self.dtype:
@@ -287,6 +308,7 @@ class PagedKV:
         """Reserve one slot per sequence for the next decode token (once per step,
         before layer 0); every layer's `decode_append` of that step then writes
         its new K/V row there."""
+        self._refuse_during_step("reserve_step")
         for b in range(self.table.batch):
             self.table.reserve(b, 1)
         self._step = (self.table.version, set(range(self.layers)))
@@ -341,6 +363,7 @@ class PagedKV:
         Split): the dropped span's pages are freed and the kept suffix's keys are
         re-rotated in place by -(c0 - a) positions in every layer. Returns the
         freed page ids."""
+        self._refuse_during_step("prune")
         suffix, freed = self.table.prune(b, s.a, s.c0, s.c)
         gap = s.c0 - s.a
         tiles = tiles_of(suffix)

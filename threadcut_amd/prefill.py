@@ -20,11 +20,14 @@ GROUPS = (1, 2, 4, 8)
 
 
 def supports(query, key, attention_mask):
-    """True if ``prefill_attention`` takes this call: a GPU call with head_dim 128,
-    g in (1, 2, 4, 8) and no mask or a boolean mask [b|1, 1, q, n]."""
+    """True if ``prefill_attention`` takes this call: a GPU call in float16 or
+    bfloat16 with head_dim 128, g in (1, 2, 4, 8) and no mask or a boolean mask
+    [b|1, 1, q, n]."""
     b, hq, q, d = query.shape
     hkv = key.shape[1]
     if not query.is_cuda or d != HEAD_DIM or hq % hkv or hq // hkv not in GROUPS:
+        return False
+    if query.dtype not in _lib.DTYPES or key.dtype != query.dtype:
         return False
     if attention_mask is None:
         return True

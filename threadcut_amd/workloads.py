@@ -59,6 +59,17 @@ def layer_caches(seed, layers, n, kv_heads=8, head_dim=128, batch=1, dtype=torch
     return ks, vs
 
 
+def sweep_layers(n, layers=36, seed=2, device="cpu"):
+    """The 36-layer decode sweep at n tokens: (queries, keys, values), per layer its own K/V
+    [1, 8, n, 128] fp16 (drawn layer by layer, K then V) and its own query grouped as
+    [1, 8, 4, 128] (the 4 query heads of each KV head), drawn afterwards from a second
+    generator of the same seed."""
+    ks, vs = layer_caches(seed, layers, n, device=device)
+    g = _gen(seed, device)
+    qs = [randn((1, 8, 4, 128), g, torch.float16, device) for _ in range(layers)]
+    return qs, ks, vs
+
+
 def inv_freq(theta=1e6, head_dim=128):
     """transformers' default RoPE inverse frequencies, float32 [head_dim / 2]."""
     return (1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))).float()
