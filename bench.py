@@ -10,10 +10,17 @@ as one HIP graph. Inputs are resident in HBM before the timed region.
 Printed JSON line:
 - value: algorithmic GB/s of the whole step (K+V read, Q read, O written:
   10240*4096 + 16384 bytes per call), us_per_call next to it;
-- roofline: the partial kernel alone, algorithmic bytes per launch over its
-  mean duration from HIP events around a graph of 36 partial launches;
+- roofline: the partial kernel alone with the tile schedule of the timed call
+  (tiles dealt round-robin over the splits), algorithmic bytes per launch
+  over its mean duration from HIP events around a graph of 36 partial
+  launches; the partial + combine fraction beside it;
+- yardstick: the partial kernel's loads alone (same grid, schedule and loads
+  in flight, no compute, nothing written) over the same 36 layers, the
+  streaming floor of that access pattern;
 - cpu_baseline: the reference's CPU decode path (torch SDPA with the query
-  heads folded, fp16, threadcut/attention.py:40-42) on the host cores;
+  heads folded, fp16, threadcut/attention.py:40-42) on os.cpu_count() host
+  threads, the fp32 form of the same call beside it, and the host's core
+  counts and CPU model;
 - splice: the 36-layer suffix splice (Split(2048, 8668, 5668), 14336-token
   caches, theta 1e6) in one launch, algorithmic GB/s (C of K and V read and
   written), with the reference's CPU splice (torch ops per layer) timed on the
@@ -86,31 +93,91 @@ def capture(fn):
     return g
 
 
+def host_info():
+    """The host the CPU baselines run on: core counts as the OS and the cgroup report them, and
+    the CPU model from lscpu."""
+    import subprocess
+
+    info = {"os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        info["cgroup_cpus"] = None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        info["cgroup_cpus"] = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        info["model"] = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")),
+                             None)
+    except (OSError, subprocess.SubprocessError):
+        info["model"] = None
+    return info
+
+
+def _median_time(fn, seconds, min_runs=5):
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_baseline(n, seconds):
-    """The reference's CPU decode path on one call of the workload, bounded to ~`seconds`."""
+    """The reference's CPU decode path on one call of the workload (fp16, torch SDPA with the
+    query heads folded, threadcut/attention.py:40-42), and the fp32 oracle form of the same
+    call beside it, each bounded to about `seconds`; os.cpu_count() threads."""
     import torch
 
     from oracle.decode import folded_sdpa
     from threadcut_amd import workloads
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     q, k, v, _ = workloads.decode_inputs(2, n=n)
     scale = D ** -0.5
     for _ in range(3):
         folded_sdpa(q, k, v, scale)
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        folded_sdpa(q, k, v, scale)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    t = times[len(times) // 2]
+    t, runs = _median_time(lambda: folded_sdpa(q, k, v, scale), seconds)
+    q32, k32, v32 = q.float(), k.float(), v.float()
+    for _ in range(2):
+        folded_sdpa(q32, k32, v32, scale)
+    t32, runs32 = _median_time(lambda: folded_sdpa(q32, k32, v32, scale), seconds / 2)
     return {"value": round(decode_bytes(n) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} single decode calls (q [1,32,1,128], K/V [1,8,{n},128] fp16) of the "
-                      f"reference's CPU path (torch SDPA, query heads folded), median {t * 1e6:.1f} us/call",
-            "us_per_call": round(t * 1e6, 2)}
+            "sample": f"{runs} single decode calls (q [1,32,1,128], K/V [1,8,{n},128] fp16) of the reference's "
+                      f"CPU path (torch SDPA, query heads folded), median {t * 1e6:.1f} us/call",
+            "us_per_call": round(t * 1e6, 2),
+            "fp32_oracle_us_per_call": round(t32 * 1e6, 2), "fp32_oracle_runs": runs32,
+            "host": host_info()}
+
+
+def cpu_ragged_baseline(seconds):
+    """The ragged batch of 16 on the host: the reference's CPU decode (fp16 folded SDPA) once per
+    sequence over its own lengths, the whole batch per sample, bounded to about `seconds`."""
+    import torch
+
+    from oracle.decode import folded_sdpa
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    lens = torch.randint(1024, 32769, (16,), generator=torch.Generator().manual_seed(3)).tolist()
+    g = torch.Generator().manual_seed(3)
+    seqs = [(torch.randn((1, HQ, 1, D), generator=g).half(), torch.randn((1, HKV, m, D), generator=g).half(),
+             torch.randn((1, HKV, m, D), generator=g).half()) for m in lens]
+    scale = D ** -0.5
+
+    def batch():
+        for q, k, v in seqs:
+            folded_sdpa(q, k, v, scale)
+
+    batch()
+    t, runs = _median_time(batch, seconds, min_runs=3)
+    nbytes = sum(lens) * 2 * HKV * D * 2 + 16 * 2 * HQ * D * 2
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_call": round(t * 1e6, 1),
+            "sample": f"{runs} passes over the 16 sequences (lengths U[1024, 32768], seed 3), one fp16 folded "
+                      f"SDPA per sequence, median per pass"}
 
 
 def cpu_splice_baseline(seconds, layers=4):
@@ -121,7 +188,7 @@ def cpu_splice_baseline(seconds, layers=4):
     from oracle.splice import splice_growing_torch
     from threadcut_amd import workloads
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     s = workloads.SPLICE_SPLIT
     ks, vs = workloads.layer_caches(1, layers, workloads.SPLICE_TOKENS)
@@ -182,21 +249,39 @@ SWEEP = (1536, 4096, 10240, 14336)
 def summarize(r, nbytes):
     us = r["ms"] * 1e3 / LAYERS
     pus = r["ms_partial"] * 1e3 / LAYERS
+    yus = r["ms_yardstick"] * 1e3 / LAYERS
     return {"us_per_call": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
             "partial_us": round(pus, 3), "partial_GB/s": round(nbytes / pus / 1e3, 1),
+            "yardstick_us": round(yus, 3), "partial_over_yardstick": round(pus / yus, 4),
             "splits": r["splits"], "split_tokens": r["split_tokens"]}
 
 
+def stream_read_lib():
+    """The measurement library (threadcut_amd/csrc/bench): the streaming-read yardstick."""
+    import ctypes
+
+    from threadcut_amd import build
+
+    lib = ctypes.CDLL(build.BENCH_LIB)
+    lib.tc_bench_stream_read.restype = ctypes.c_int
+    lib.tc_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
+                                         ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
 def measure_sweep(dev, n, steps, warmup, split, only):
-    """36 sequential decode calls at n tokens (own K/V per layer) as one HIP graph."""
+    """36 sequential decode calls at n tokens (own K/V per layer) as one HIP graph; the
+    partial pass alone and the streaming-read yardstick as graphs over the same layers."""
     import torch
 
-    from threadcut_amd import flash_decode, workloads
+    from threadcut_amd import _lib, flash_decode, workloads
 
     qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
     outs = [torch.empty_like(q) for q in qs]
     plans = [flash_decode.DecodePlan(q, k, v, D ** -0.5, o, split=split or None)
              for q, k, v, o in zip(qs, ks, vs, outs)]
+    S = plans[0].splits
 
     def step():
         for p in plans:
@@ -206,11 +291,23 @@ def measure_sweep(dev, n, steps, warmup, split, only):
         for p in plans:
             p.run_partial()
 
-    result = {"splits": plans[0].splits, "split_tokens": plans[0].split_tokens}
+    result = {"splits": S, "split_tokens": plans[0].split_tokens}
     if only in (None, "decode"):
         result["ms"] = time_graph(capture(step), steps, warmup)
     if only in (None, "partial"):
         result["ms_partial"] = time_graph(capture(step_partial), steps, warmup)
+    if only in (None, "yardstick"):
+        ylib = stream_read_lib()
+        sink = torch.zeros(S * HKV, dtype=torch.int32, device=dev)
+        st = [(_lib.i64x2(k.stride(1), k.stride(2)), _lib.i64x2(v.stride(1), v.stride(2))) for k, v in zip(ks, vs)]
+
+        def step_read():
+            s_ = _lib.stream_of(dev)
+            for (k, v), (kst, vst) in zip(zip(ks, vs), st):
+                if ylib.tc_bench_stream_read(k.data_ptr(), v.data_ptr(), kst, vst, n, HKV, S, sink.data_ptr(), s_):
+                    raise RuntimeError("tc_bench_stream_read failed")
+
+        result["ms_yardstick"] = time_graph(capture(step_read), steps, warmup)
     del plans, ks, vs
     torch.cuda.empty_cache()
     return result
@@ -523,11 +620,14 @@ def measure_paged(dev, n, steps, page_tokens=64):
 
     # One decode step with the new token's K/V: written into its reserved slot by
     # two torch row copies per layer and then attended, against the fused call.
-    cache.reserve_step()
-    page, slot = (int(x) for x in cache.table.token_slots(0)[-1])
-    tab, cnt, mt = cache.device_table()
+    # The step is completed once eagerly (write_step), so decode() reads the slot.
     kns = [torch.randn((1, HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
     vns = [torch.randn((1, HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+    cache.reserve_step()
+    for layer in range(LAYERS):
+        cache.write_step(layer, kns[layer], vns[layer])
+    page, slot = (int(x) for x in cache.table.token_slots(0)[-1])
+    tab, cnt, mt = cache.device_table()
     lib = _lib.load()
     S = lib.tc_decode_num_splits(1, HKV, 16 * mt, 0, 0)
     ws = torch.empty(lib.tc_decode_workspace_bytes(1, HKV, HQ // HKV, D, S), dtype=torch.uint8, device=dev)
@@ -634,7 +734,8 @@ def main():
     ap.add_argument("--no-splice", action="store_true")
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
-    ap.add_argument("--only", choices=["decode", "partial", "splice", "copy", "prefill", "decode-step", "paged"],
+    ap.add_argument("--only", choices=["decode", "partial", "yardstick", "splice", "copy", "prefill", "decode-step",
+                                       "paged"],
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -689,6 +790,7 @@ def main():
     value = LAYERS * per_call_bytes / (ms * 1e-3) / 1e9
     partial_us = result["ms_partial"] * 1e3 / LAYERS
     achieved = per_call_bytes / (partial_us * 1e-6) / 1e9
+    yard_us = result["ms_yardstick"] * 1e3 / LAYERS
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -708,11 +810,21 @@ def main():
                                f"batch 1, one HIP graph per step",
                    "layers": LAYERS, "kv_tokens": n, "batch": 1, "q_heads": HQ, "kv_heads": HKV,
                    "head_dim": D, "splits": result["splits"], "split_tokens": result["split_tokens"]},
-        "roofline": {"bound": "hbm", "kernel": "decode_partial_kernel<f16, g=4>",
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode_partial_kernel<f16, g=4>, tiles dealt round-robin over the splits "
+                               "(the schedule of tc_decode_attention)",
                      "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "us_per_launch": round(partial_us, 3),
                      "bytes_per_launch": per_call_bytes,
-                     "traffic": read_traffic(f"decode_partial_n{n}_traffic.txt")},
+                     "traffic": read_traffic(f"decode_partial_rr_n{n}_traffic.txt"),
+                     "frac_partial_plus_combine": round(value / PEAK_GBS, 4),
+                     "combine_us_per_call": round(ms * 1e3 / LAYERS - partial_us, 3)},
+        "yardstick": {"what": "the partial kernel's loads alone (same grid, tile schedule, loads in flight), "
+                              "36 distinct layers in one graph",
+                      "us_per_launch": round(yard_us, 3),
+                      "GB/s": round(per_call_bytes / (yard_us * 1e-6) / 1e9, 1),
+                      "frac": round(per_call_bytes / (yard_us * 1e-6) / 1e9 / PEAK_GBS, 4),
+                      "partial_over_yardstick": round(partial_us / yard_us, 4)},
     }
     if not args.no_reports:
         sweep = {}
@@ -734,6 +846,8 @@ def main():
         line["cpu_baseline"] = cpu_baseline(n, args.cpu_seconds)
         if "splice" in line:
             line["splice"]["cpu_baseline"] = cpu_splice_baseline(min(5.0, args.cpu_seconds))
+        if "ragged_16" in line:
+            line["ragged_16"]["cpu_baseline"] = cpu_ragged_baseline(min(5.0, args.cpu_seconds))
     print(json.dumps(line))
 
 

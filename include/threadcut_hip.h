@@ -100,6 +100,23 @@ int tc_decode_partial(const void* q_dev, const int64_t q_strides[3],
                       float scale, int split_tokens, int num_splits,
                       float* o_part_dev, float* lse_part_dev, void* stream);
 
+/* The partial pass of tc_decode_attention: the same kernel and outputs as
+ * tc_decode_partial, but the S splits share each head's 16-token tiles
+ * round-robin (split s takes the tiles of waves 4s..4s+3 in every round of
+ * 4S tiles) instead of owning contiguous slices, so the loads in flight stay
+ * adjacent in HBM. A split's partial is the softmax over its own tiles, and
+ * tc_decode_combine merges the S partials into the same output as with
+ * contiguous slices. For callers that merge partials themselves (for example
+ * after exchanging them between GPUs that hold different token ranges), and
+ * for timing the pass alone. Same arguments as tc_decode_partial. */
+int tc_decode_partial_interleaved(const void* q_dev, const int64_t q_strides[3],
+                                  const void* k_dev, const int64_t k_strides[3],
+                                  const void* v_dev, const int64_t v_strides[3],
+                                  const int32_t* lens_dev, int64_t n_tokens,
+                                  int batch, int kv_heads, int group, int head_dim, int dtype,
+                                  float scale, int split_tokens, int num_splits,
+                                  float* o_part_dev, float* lse_part_dev, void* stream);
+
 /* Combine pass only: out[b,h,g,:] = sum_s softmax_s(lse)[s] * o_part[b,h,s,g,:],
  * cast to dtype (round to nearest even). All-(-inf) lse (no tokens) gives 0.
  * Equivalent of threadcut/flash_decode.py:68-69. */

@@ -333,3 +333,48 @@ def test_gate_keeps_the_reference_path_for_other_calls(gpu, monkeypatch, dtype, 
     ref = od.attention_f64(q.float().numpy().reshape(1, hkv, hq // hkv, d), k.float().numpy(), v.float().numpy(),
                            d ** -0.5).reshape(1, 1, hq, d)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= (1e-5 if dtype == torch.float32 else TOL)
+
+
+@pytest.mark.parametrize("n,split", [(1000, 64), (10240, None)])
+def test_interleaved_partials_cover_round_robin_tiles(gpu, n, split):
+    """tc_decode_partial_interleaved: split s's partial is the softmax over the 16-token tiles
+    s*4 + w + j*4S (w < 4) of its head, in float64 within 1e-4; partial + combine is bit-identical
+    to tc_decode_attention (the same kernels and plan)."""
+    q, k, v, _ = workloads.decode_inputs(43, n=n)
+    hkv, g, d = 8, 4, 128
+    qd = q.to(gpu).reshape(1, hkv, g, d)
+    kd, vd = k.to(gpu), v.to(gpu)
+    S = flash_decode.num_splits(1, hkv, n, split)
+    T = flash_decode.split_tokens(1, hkv, n, split)
+    print(f"case: interleaved partials n={n} S={S} T={T}", flush=True)
+    o = torch.empty((1, hkv, S, g, d), dtype=torch.float32, device=gpu)
+    lse = torch.empty((1, hkv, S, g), dtype=torch.float32, device=gpu)
+    lib = _lib.load()
+    st = lambda t: _lib.i64x3(*[t.stride(i) if t.shape[i] > 1 else 0 for i in range(3)])
+    rc = lib.tc_decode_partial_interleaved(qd.data_ptr(), st(qd), kd.data_ptr(), st(kd), vd.data_ptr(), st(vd),
+                                           None, n, 1, hkv, g, d, _lib.TC_DTYPE_F16, SCALE, T, S, o.data_ptr(),
+                                           lse.data_ptr(), _lib.stream_of(gpu))
+    _lib.check(rc, "tc_decode_partial_interleaved")
+    out = torch.empty_like(qd)
+    rc = lib.tc_decode_combine(o.data_ptr(), lse.data_ptr(), 1, hkv, g, d, S, out.data_ptr(), st(out),
+                               _lib.TC_DTYPE_F16, _lib.stream_of(gpu))
+    _lib.check(rc, "tc_decode_combine")
+    ref = flash_decode.decode_attention_batched(qd, kd, vd, SCALE, split=split)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    qn, kn, vn = q.float().numpy().reshape(hkv, g, d).astype(np.float64), k[0].float().numpy(), v[0].float().numpy()
+    tiles = np.arange(-(-n // 16))
+    for s in range(S):
+        mine = tiles[(tiles // 4) % S == s]
+        toks = (mine[:, None] * 16 + np.arange(16)[None]).ravel()
+        toks = toks[toks < n]
+        if len(toks) == 0:
+            assert bool(torch.isinf(lse[0, :, s]).all())
+            continue
+        sc = np.einsum("hgd,htd->hgt", qn, kn[:, toks].astype(np.float64)) * SCALE
+        m = sc.max(-1, keepdims=True)
+        p = np.exp(sc - m)
+        want_o = np.einsum("hgt,htd->hgd", p / p.sum(-1, keepdims=True), vn[:, toks].astype(np.float64))
+        want_l = (m[..., 0] + np.log(p.sum(-1)))
+        assert np.abs(o[0, :, s].cpu().numpy() - want_o).max() <= 1e-4
+        assert np.abs(lse[0, :, s].cpu().numpy() - want_l).max() <= 1e-4

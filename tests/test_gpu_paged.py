@@ -275,3 +275,30 @@ def test_decode_and_prune_refused_while_a_step_is_pending(gpu):
     cache.decode(1, q, SCALE)  # the step is complete
     cache.prune(0, Split(10, 20, 30), workloads.inv_freq())
     assert cache.length(0) == 40
+
+
+def test_write_step_then_decode_reads_the_new_rows(gpu):
+    """The unfused step order: write_step() puts each layer's new row into its reserved slot
+    with torch copies; decode() then attends it like any cached token."""
+    cache, host = filled(gpu, 2, [50, 9], 16, 72)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(72)
+    q = torch.randn((2, 8, 4, 128), generator=g, device=gpu).half()
+    kn = [torch.randn((2, 8, 128), generator=g, device=gpu).half() for _ in range(2)]
+    vn = [torch.randn((2, 8, 128), generator=g, device=gpu).half() for _ in range(2)]
+    cache.reserve_step()
+    with pytest.raises(RuntimeError, match="no reserved slot"):
+        cache.write_step(5, kn[0], vn[0])
+    for layer in range(2):
+        cache.write_step(layer, kn[layer], vn[layer])
+    with pytest.raises(RuntimeError, match="no reserved slot"):
+        cache.write_step(0, kn[0], vn[0])
+    for layer in range(2):
+        out = cache.decode(layer, q, SCALE)
+        torch.cuda.synchronize()
+        for b in range(2):
+            k, v = host[b][layer]
+            k = torch.cat((k, kn[layer][b].cpu()[:, None]), 1)
+            v = torch.cat((v, vn[layer][b].cpu()[:, None]), 1)
+            want = closed_form(q[b:b + 1].cpu(), k[None], v[None])
+            assert np.abs(out[b:b + 1].float().cpu().numpy() - want).max() <= TOL[torch.float16]

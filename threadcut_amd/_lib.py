@@ -46,6 +46,8 @@ SIGNATURES = {
     "tc_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "tc_decode_partial": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I,
                                _P, _P, _P]),
+    "tc_decode_partial_interleaved": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
+                                           _I, _P, _P, _P]),
     "tc_decode_combine": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _I64P, _I, _P]),
     "tc_decode_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64, _I, _I, _I, _I, _I, _F, _I,
                                  _P, _S, _P, _I64P, _P]),

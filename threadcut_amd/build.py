@@ -3,7 +3,9 @@
 Compiles every ``csrc/*.hip`` source with hipcc (and the host-only
 ``csrc/*.cpp`` with g++) into ``_build/*.o`` in parallel, and links
 ``libthreadcut_hip.so`` next to this file, where
-``threadcut_amd._lib`` loads it. Run as ``python -m threadcut_amd.build``.
+``threadcut_amd._lib`` loads it. The measurement kernels of ``csrc/bench/``
+(not part of the decode ABI) link into ``libthreadcut_bench.so`` beside it.
+Run as ``python -m threadcut_amd.build``.
 """
 import concurrent.futures
 import glob
@@ -16,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libthreadcut_hip.so")
+BENCH_LIB = os.path.join(HERE, "libthreadcut_bench.so")
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms stay off: the kernels are written for scalar fp32.
@@ -47,21 +50,28 @@ def _compile(src, obj):
     return err
 
 
-def build(verbose=False):
-    """Compile and link the library; returns its path. Always rebuilds."""
-    os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
-    objs = [os.path.join(BUILD, os.path.splitext(os.path.basename(s))[0] + ".o") for s in sources]
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        for src, warn in zip(sources, ex.map(_compile, sources, objs)):
-            if warn and verbose:
-                print(f"[{os.path.basename(src)}]\n{warn}", file=sys.stderr)
-    tmp = LIB + ".tmp"
+def _link(objs, lib):
+    tmp = lib + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose=False):
+    """Compile and link both libraries; returns the decode library's path. Always rebuilds."""
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
+    bench_sources = sorted(glob.glob(os.path.join(CSRC, "bench", "*.hip")))
+    every = sources + bench_sources
+    objs = [os.path.join(BUILD, os.path.splitext(os.path.basename(s))[0] + ".o") for s in every]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(every))) as ex:
+        for src, warn in zip(every, ex.map(_compile, every, objs)):
+            if warn and verbose:
+                print(f"[{os.path.basename(src)}]\n{warn}", file=sys.stderr)
+    _link(objs[:len(sources)], LIB)
+    _link(objs[len(sources):], BENCH_LIB)
     return LIB
 
 

@@ -1,0 +1,94 @@
+// Streaming-read yardstick for the decode partial kernel (measurement only;
+// not part of the decode ABI). It issues exactly the partial kernel's loads
+// and nothing else: grid (S splits, Hkv heads), 256 threads, each wave
+// taking 16-token tiles s*4 + w, + 4S, ... of its head (the round-robin
+// schedule of tc_decode_attention), per lane and tile four 16-byte K loads
+// (token lane % 16, bytes 64 i + 16 (lane / 16)) and four 16-byte V loads
+// (tokens 4 (lane / 16) + j, bytes 16 (lane % 16)), two tiles in flight,
+// non-temporal. The loaded words are folded into one value that is stored
+// only if it equals a constant, so the loads stay live and nothing is written.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+struct Args {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t sk_h, sk_t, sv_h, sv_t;  // element strides (head, token)
+  int n, splits;
+  uint32_t* sink;
+};
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const Args a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nl = lane & 15, g = lane >> 4;
+  const int s = blockIdx.x, h = blockIdx.y;
+  const int row_k = static_cast<int>(a.sk_t) * 2, row_v = static_cast<int>(a.sv_t) * 2;
+  const char* kslab = reinterpret_cast<const char*>(a.k + h * a.sk_h);
+  const char* vslab = reinterpret_cast<const char*>(a.v + h * a.sv_h);
+  const __amdgpu_buffer_rsrc_t rk = rsrc(kslab, a.n * row_k);
+  const __amdgpu_buffer_rsrc_t rv = rsrc(vslab, a.n * row_v);
+  int koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    koff[i] = nl * row_k + 64 * i + 16 * g;
+    voff[i] = (4 * g + i) * row_v + 16 * nl;
+  }
+  const int step = a.splits * 4 * 16;  // tokens between a wave's tiles
+  int tok = (s * 4 + wave) * 16;
+  u32x4 t0[8], t1[8];
+  auto load = [&](u32x4* t, int t0k) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      t[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, t0k * row_k + koff[i], 0, 2);
+      t[4 + i] = __builtin_amdgcn_raw_buffer_load_b128(rv, t0k * row_v + voff[i], 0, 2);
+    }
+  };
+  uint32_t acc = 0;
+  auto fold = [&](const u32x4* t) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc ^= t[i].x ^ t[i].y ^ t[i].z ^ t[i].w;
+  };
+  load(t0, tok);
+  while (tok < a.n) {
+    load(t1, tok + step);
+    fold(t0);
+    tok += step;
+    if (tok >= a.n) break;
+    load(t0, tok + step);
+    fold(t1);
+    tok += step;
+  }
+  if (acc == 0x9e3779b9u) a.sink[blockIdx.y * gridDim.x + blockIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+// One launch over K/V [Hkv, n, 128] (element strides head, token; last dim
+// contiguous) with `splits` work-groups per head. Returns 0 or 1 (bad
+// arguments or launch failure). `sink` holds splits * kv_heads words.
+int tc_bench_stream_read(const void* k, const void* v, const int64_t k_strides[2], const int64_t v_strides[2],
+                         int n_tokens, int kv_heads, int splits, void* sink, void* stream) {
+  if (!k || !v || !sink || n_tokens < 1 || kv_heads < 1 || splits < 1 || splits > 65535 || kv_heads > 65535)
+    return 1;
+  if (k_strides[1] < 128 || v_strides[1] < 128) return 1;
+  if (static_cast<int64_t>(n_tokens + 16 * 4 * splits) * k_strides[1] * 2 >= (int64_t(1) << 31) ||
+      static_cast<int64_t>(n_tokens + 16 * 4 * splits) * v_strides[1] * 2 >= (int64_t(1) << 31))
+    return 1;
+  Args a{static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), k_strides[0], k_strides[1],
+         v_strides[0], v_strides[1], n_tokens, splits, static_cast<uint32_t*>(sink)};
+  hipLaunchKernelGGL(stream_read_kernel, dim3(splits, kv_heads), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+}  // extern "C"

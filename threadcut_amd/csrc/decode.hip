@@ -821,6 +821,17 @@ int tc_decode_partial(const void* q_dev, const int64_t q_strides[3], const void*
                       stream);
 }
 
+int tc_decode_partial_interleaved(const void* q_dev, const int64_t q_strides[3], const void* k_dev,
+                                  const int64_t k_strides[3], const void* v_dev, const int64_t v_strides[3],
+                                  const int32_t* lens_dev, int64_t n_tokens, int batch, int kv_heads, int group,
+                                  int head_dim, int dtype, float scale, int split_tokens, int num_splits,
+                                  float* o_part_dev, float* lse_part_dev, void* stream) {
+  clear_error();
+  return partial_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, lens_dev, n_tokens, batch, kv_heads, group,
+                      head_dim, dtype, scale, split_tokens, num_splits, o_part_dev, lse_part_dev, 1, nullptr,
+                      stream);
+}
+
 int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int batch, int kv_heads, int group,
                       int head_dim, int num_splits, void* out_dev, const int64_t out_strides[3], int dtype,
                       void* stream) {

@@ -244,6 +244,12 @@ class DecodePlan:
         _lib.check(self.lib.tc_decode_attention(*self.args, s), "tc_decode_attention")
 
     def run_partial(self, stream=None):
+        """The partial pass alone, with the round-robin tile schedule ``run()`` uses."""
+        s = stream if stream is not None else _lib.stream_of(self.device)
+        _lib.check(self.lib.tc_decode_partial_interleaved(*self.partial_args, s), "tc_decode_partial_interleaved")
+
+    def run_partial_contiguous(self, stream=None):
+        """The partial pass with contiguous splits (the reference's slicing)."""
         s = stream if stream is not None else _lib.stream_of(self.device)
         _lib.check(self.lib.tc_decode_partial(*self.partial_args, s), "tc_decode_partial")
 

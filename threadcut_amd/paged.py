@@ -313,6 +313,22 @@ class PagedKV:
             self.table.reserve(b, 1)
         self._step = (self.table.version, set(range(self.layers)))
 
+    def write_step(self, layer, k_new, v_new):
+        """The unfused order of a decode step: write one layer's new K/V rows ([B, Hkv, D] or
+        [B, Hkv, 1, D]) into the slots reserve_step() took, with two torch row copies. After
+        every layer is written (here or by decode_append), decode() reads the new token."""
+        step = getattr(self, "_step", None)
+        if step is None or step[0] != self.table.version or layer not in step[1]:
+            raise RuntimeError(f"PagedKV.write_step: layer {layer} has no reserved slot in this step")
+        b = self.table.batch
+        kn = k_new.reshape(b, self.kv_heads, HEAD_DIM)
+        vn = v_new.reshape(b, self.kv_heads, HEAD_DIM)
+        for i in range(b):
+            page, slot = (int(x) for x in self.table.token_slots(i)[-1])
+            self.k_pools[layer][page, :, slot] = kn[i]
+            self.v_pools[layer][page, :, slot] = vn[i]
+        step[1].discard(layer)
+
     def decode_append(self, layer, q, k_new, v_new, scale, out=None, split=None):
         """One decode step of one layer with the append fused in: k_new/v_new
         [B, Hkv, D] (or [B, Hkv, 1, D]) go to the slots `reserve_step` took, and q
