@@ -151,7 +151,7 @@ def decode_calls(monkeypatch):
     return calls
 
 
-@pytest.mark.parametrize("growing", [False, True])
+@pytest.mark.parametrize("growing", [False, True, "slab"])
 @torch.no_grad()
 def test_T2_splice_matches_fresh_compute(growing, decode_calls):
     """tests/test_core.py:77-90 with the "threadcut" attention on the CPU: a cache A·B·C (C placed
@@ -167,7 +167,7 @@ def test_T2_splice_matches_fresh_compute(growing, decode_calls):
             lr.keys, lr.values = torch.cat((lr.keys, lc.keys), 2), torch.cat((lr.values, lc.values), 2)
         ref_logits = forward_chunks(m, D, ref, chunk)
         parts = [kv_alone(m, A, 0), kv_alone(m, B, len(A)), kv_alone(m, C, len(A) + len(B))]
-        cache = kv.new_cache(m.config) if growing else DynamicCache(config=m.config)
+        cache = kv.new_cache(m.config, slab=growing == "slab") if growing else DynamicCache(config=m.config)
         for i, layer in enumerate(cache.layers):
             layer.update(torch.cat([p.layers[i].keys for p in parts], 2),
                          torch.cat([p.layers[i].values for p in parts], 2))
@@ -198,3 +198,26 @@ def test_decode_steps_match_stock_sdpa(decode_calls):
         b = m(input_ids=torch.tensor([[t]]), past_key_values=c2, use_cache=True).logits[0, -1]
         assert torch.allclose(a, b, atol=1e-5, rtol=0)
     assert len(decode_calls) == 2 * len(steps)  # 2 layers per step, all through the decode branch
+
+
+def test_slab_layers_share_one_allocation_through_growth():
+    """new_cache(slab=True) on the host: the layers' buffers are views of one [L, 2, B, Hkv, cap, D]
+    tensor before and after a growth, and each layer keeps its own tokens."""
+    cfg = Qwen3Config(num_hidden_layers=3, head_dim=16, num_key_value_heads=2)
+    cache = kv.new_cache(cfg, slab=True)
+    g = torch.Generator().manual_seed(5)
+    rows = [(torch.randn(1, 2, 2000, 16, generator=g), torch.randn(1, 2, 2000, 16, generator=g)) for _ in range(3)]
+    for layer, (k, v) in zip(cache.layers, rows):
+        layer.update(k, v)
+    t = cache.layers[0].slab.tensor
+    assert t.shape == (3, 2, 1, 2, 2048, 16)
+    for layer, (k, v) in zip(cache.layers, rows):
+        layer.update(k[:, :, :100], v[:, :, :100])  # past 2048: grows once, for every layer
+    t2 = cache.layers[0].slab.tensor
+    assert t2.shape[-2] == 4096 and t2.untyped_storage().data_ptr() != t.untyped_storage().data_ptr()
+    for i, (layer, (k, v)) in enumerate(zip(cache.layers, rows)):
+        assert layer.kbuf.untyped_storage().data_ptr() == t2.untyped_storage().data_ptr()
+        assert layer.kbuf.data_ptr() == t2[i, 0].data_ptr() and layer.vbuf.data_ptr() == t2[i, 1].data_ptr()
+        assert layer.keys.shape == (1, 2, 2100, 16)
+        assert torch.equal(layer.keys, torch.cat((k, k[:, :, :100]), 2))
+        assert torch.equal(layer.values, torch.cat((v, v[:, :, :100]), 2))

@@ -138,3 +138,47 @@ def test_fused_append_cache_matches_plain_cache(model):
         assert lf.n == n == s.a + s.c
         assert np.array_equal(lf.keys.cpu().numpy(), kw[..., :n, :])
         assert np.array_equal(lf.values.cpu().numpy(), vw[..., :n, :])
+
+
+@torch.no_grad()
+def test_slab_cache_matches_per_layer_buffers(model):
+    """new_cache(slab=True): every layer's buffers are views of one [L, 2, B, Hkv, cap, D]
+    allocation. Prefill, fused-append decode steps across a capacity growth, a splice (one
+    tc_splice_rope over the slab's views) and a captured decode step give the per-layer cache's
+    results: bit-identical cache rows, identical logits."""
+    from threadcut_amd.graph import DecodeGraph
+
+    ids = rand_ids(2100, 8)
+    slab = kv.new_cache(model.config, fused_append=True, slab=True)
+    per = kv.new_cache(model.config, fused_append=True)
+    a = run(model, ids[:2040], slab, attention.NAME)
+    b = run(model, ids[:2040], per, attention.NAME)
+    assert torch.equal(a, b)
+    store = slab.layers[0].slab.tensor
+    assert store.shape[:2] == (2, 2) and store.shape[-2] == 2048
+    for i, layer in enumerate(slab.layers):
+        assert layer.kbuf.data_ptr() == store[i, 0].data_ptr() and layer.vbuf.data_ptr() == store[i, 1].data_ptr()
+    for t in ids[2040:2060]:  # crosses capacity 2048: the slab grows once for both layers
+        a = run(model, [t], slab, attention.NAME)
+        b = run(model, [t], per, attention.NAME)
+        assert torch.equal(a, b)
+    grown = slab.layers[0].slab.tensor
+    assert grown.shape[-2] > 2048 and all(l.kbuf.data_ptr() == grown[i, 0].data_ptr()
+                                         for i, l in enumerate(slab.layers))
+    inv = model.model.rotary_emb.inv_freq
+    s = kv.Split(100, 700, 1300)
+    kv.splice(slab, s, inv)
+    kv.splice(per, s, inv)
+    for ls, lp in zip(slab.layers, per.layers):
+        assert torch.equal(ls.keys, lp.keys) and torch.equal(ls.values, lp.values)
+    dg_s = DecodeGraph(model, slab, max_new_tokens=4)
+    dg_p = DecodeGraph(model, per, max_new_tokens=4)
+    for t in ids[2060:2064]:
+        a = dg_s.step([t]).float().clone()
+        b = dg_p.step([t]).float().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+    dg_s.close()
+    dg_p.close()
+    for ls, lp in zip(slab.layers, per.layers):
+        assert torch.equal(ls.keys, lp.keys)

@@ -224,6 +224,47 @@ def _splice_index_select_torch(layers, s, inv_freq):
         layer.keys, layer.values = k, v
 
 
+class KVSlab:
+    """One allocation [L, 2, B, Hkv, cap, D] holding every layer's K and V buffers.
+
+    Layer l's buffers are the views ``slab[l, 0]`` and ``slab[l, 1]``, each a
+    contiguous [B, Hkv, cap, D] tensor like a GrowingLayer's own, so kernels,
+    the splice's pointer table and the engine's ``layer.keys`` views see the
+    same layout. Capacity grows for all layers at once (the GrowingLayer rule,
+    max(need, 1.25 cap, cap + 2048)), with one copy of each layer's tokens.
+    """
+
+    def __init__(self, layers):
+        self.layers = layers
+        self.tensor = None
+
+    @property
+    def capacity(self):
+        return 0 if self.tensor is None else self.tensor.shape[-2]
+
+    def reserve(self, need, like):
+        """Grow to hold `need` tokens per layer (like: a [B, Hkv, *, D] tensor of the cache's type)."""
+        cap = self.capacity
+        if need <= cap:
+            return
+        for layer in self.layers:
+            if getattr(layer, "kbuf", None) is not None:
+                layer.flush()
+        new = max(need, int(cap * 1.25), cap + 2048)
+        b, h, d = like.shape[0], like.shape[1], like.shape[-1]
+        t = like.new_empty((len(self.layers), 2, b, h, new, d))
+        for i, layer in enumerate(self.layers):
+            n = getattr(layer, "n", 0) if getattr(layer, "kbuf", None) is not None else 0
+            if n:
+                t[i, 0, :, :, :n] = layer.kbuf[..., :n, :]
+                t[i, 1, :, :, :n] = layer.vbuf[..., :n, :]
+        self.tensor = t
+        for i, layer in enumerate(self.layers):
+            if getattr(layer, "kbuf", None) is not None:
+                layer.kbuf, layer.vbuf = t[i, 0], t[i, 1]
+                layer._view()
+
+
 class GrowingLayer(DynamicLayer):
     """DynamicLayer backed by a preallocated buffer (threadcut/kv.py:44-92).
 
@@ -239,6 +280,9 @@ class GrowingLayer(DynamicLayer):
 
     fused_append = False
     pending = None
+    # Set by new_cache(slab=True): the shared KVSlab and this layer's index in it.
+    slab = None
+    slab_index = 0
     # Set by graph.DecodeGraph: an int32 [B] device tensor holding the token
     # count, so the decode kernel takes the append position from the device
     # (tc_decode_append_attention_at) instead of from the host-side n.
@@ -267,6 +311,12 @@ class GrowingLayer(DynamicLayer):
             self.pending = None
 
     def _reserve(self, need, like):
+        if self.slab is not None:
+            self.slab.reserve(need, like)
+            if self.kbuf is None:
+                t = self.slab.tensor
+                self.kbuf, self.vbuf = t[self.slab_index, 0], t[self.slab_index, 1]
+            return
         cap = 0 if self.kbuf is None else self.kbuf.shape[-2]
         if need <= cap:
             return
@@ -319,14 +369,18 @@ class GrowingLayer(DynamicLayer):
         self._view()
 
 
-def new_cache(config, fused_append=False):
+def new_cache(config, fused_append=False, slab=False):
     """A DynamicCache whose layers are GrowingLayers (threadcut/kv.py:95-98).
 
     fused_append=True defers single-token appends into the decode attention
     kernel; use it only with the "threadcut" attention implementation.
+    slab=True keeps every layer's buffers in one [L, 2, B, Hkv, cap, D]
+    allocation (KVSlab) that grows for all layers at once.
     """
     cache = DynamicCache(config=config)
     cache.layers = [GrowingLayer() for _ in cache.layers]
-    for layer in cache.layers:
+    shared = KVSlab(cache.layers) if slab else None
+    for i, layer in enumerate(cache.layers):
         layer.fused_append = fused_append
+        layer.slab, layer.slab_index = shared, i
     return cache
