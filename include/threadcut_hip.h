@@ -249,6 +249,30 @@ int tc_decode_paged_append_attention(const void* q_dev, const int64_t q_strides[
                                      int split_tokens, void* workspace_dev, size_t workspace_bytes,
                                      void* out_dev, const int64_t out_strides[3], void* stream);
 
+/* The same step with the sequence lengths on the device, so that one captured
+ * HIP graph serves every step (the per-token loop of threadcut/engine.py:88-95
+ * over a paged cache; no counterpart in the reference). Sequence b holds
+ * lens_dev[b] tokens before the step; its new token goes to logical position
+ * lens_dev[b], whose row sits tok_off_dev[b * tok_pitch + lens_dev[b]] bytes
+ * into the head slab of the pools (an offset outside the pool writes
+ * nothing). The tile table covers slots reserved ahead: each entry's 4th word
+ * is its first logical position, and only rows below lens_dev[b] are read.
+ * The split plan depends on max_tiles only, so the caller advances lens_dev
+ * between steps (on the device, inside the graph) and nothing else changes.
+ * Pools must be under 2 GiB (32-bit offsets). Workspace as
+ * tc_decode_paged_attention. */
+int tc_decode_paged_append_attention_at(const void* q_dev, const int64_t q_strides[3],
+                                        void* k_pool_dev, void* v_pool_dev,
+                                        const int64_t pool_strides[3], int num_pages, int page_tokens,
+                                        const int32_t* tile_table_dev, const int32_t* tiles_dev,
+                                        int64_t max_tiles, const int32_t* tok_off_dev, int64_t tok_pitch,
+                                        const int32_t* lens_dev, const void* k_new_dev,
+                                        const int64_t k_new_strides[2], const void* v_new_dev,
+                                        const int64_t v_new_strides[2], int batch, int kv_heads,
+                                        int group, int head_dim, int dtype, float scale,
+                                        int split_tokens, void* workspace_dev, size_t workspace_bytes,
+                                        void* out_dev, const int64_t out_strides[3], void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* RoPE delta-shift and suffix splice                                        */
 /*                                                                           */
@@ -343,6 +367,26 @@ int tc_prefill_attention(const void* q, const int64_t q_strides[3],
                          int head_dim, int dtype, float scale,
                          int num_splits, void* workspace, size_t workspace_bytes,
                          void* out, const int64_t out_strides[3], void* stream);
+
+/* tc_prefill_attention over a paged cache: the prefill branch of
+ * threadcut/attention.py:43-46 for a cache kept in page pools (the layout the
+ * reference's README.md:141-144 proposes). K and V are pools [pages, Hkv, P,
+ * D] with element strides pool_strides {page, head, slot}; sequence b's
+ * logical key t (t < n_tokens) is the row tok_off_dev[b * tok_pitch + t]
+ * bytes into a head's slab (the same offset in K and V). Keys keep their
+ * logical order, so masks, is_causal and the tile map mean what they mean
+ * for tc_prefill_attention, whose other arguments this takes unchanged.
+ * Pools must be under 2 GiB (32-bit offsets); an offset outside the pool
+ * reads zeros. */
+int tc_prefill_paged_attention(const void* q, const int64_t q_strides[3],
+                               const void* k_pool, const void* v_pool, const int64_t pool_strides[3],
+                               int num_pages, const int32_t* tok_off, int64_t tok_pitch,
+                               const uint8_t* mask, const int64_t mask_strides[3],
+                               const uint8_t* mask_tiles, size_t mask_tiles_bytes, int causal,
+                               int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
+                               int head_dim, int dtype, float scale,
+                               int num_splits, void* workspace, size_t workspace_bytes,
+                               void* out, const int64_t out_strides[3], void* stream);
 
 /* Key splits tc_prefill_attention uses with num_splits <= 0 (a negative value
  * is -TC_ERR_*): 1 when the query blocks (128 rows of one KV head each) give

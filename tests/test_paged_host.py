@@ -29,11 +29,18 @@ def check_table(t, model):
         assert cnt[b] == len(ts)
         rows = []
         for (page, slot, n), e in zip(ts, tab[b].tolist()):
-            assert tuple(e) == (page, slot, n, 0)
+            assert tuple(e) == (page, slot, n, len(rows))  # the 4th word: the tile's first logical position
             assert 1 <= n <= TILE and slot + n <= t.page_tokens
             assert slot // TILE == (slot + n - 1) // TILE  # a tile never crosses a 16-slot boundary
             rows += [(page, slot + i) for i in range(n)]
         assert rows == model[b]
+    # Byte offsets of every token's row in a head slab (page stride 1000 B, slot stride 10 B here).
+    off = t.token_offsets(1000, 10, pitch=5)
+    assert off.dtype == np.int32 and off.shape[1] >= max([5] + [len(m) for m in model])
+    for b in range(t.batch):
+        want = [p * 1000 + s_ * 10 for p, s_ in model[b]]
+        assert off[b, :len(want)].tolist() == want
+        assert (off[b, len(want):] == np.iinfo(np.int32).min).all()
 
 
 @pytest.mark.parametrize("page_tokens", [16, 64, 40])

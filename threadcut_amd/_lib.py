@@ -61,6 +61,9 @@ SIGNATURES = {
                                        _P, _S, _P, _I64P, _P]),
     "tc_decode_paged_append_attention": (_I, [_P, _I64P, _P, _P, _I64P, _I, _I, _P, _P, _I64, _P, _I64P, _P,
                                               _I64P, _I, _I, _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
+    "tc_decode_paged_append_attention_at": (_I, [_P, _I64P, _P, _P, _I64P, _I, _I, _P, _P, _I64, _P, _I64, _P,
+                                                 _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _F, _I, _P, _S, _P,
+                                                 _I64P, _P]),
     "tc_shift_keys": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I64, _I, _I, _FP, _P]),
     "tc_splice_rope": (_I, [_PP, _PP, _I, _I64P, _I, _I, _I64, _I, _I, _I64, _I64, _I64, _FP, _P]),
     "tc_splice_copy": (_I, [_PP, _PP, _I64P, _I64, _PP, _PP, _I64P, _I, _I, _I, _I, _I, _I64, _I64, _I64,
@@ -68,6 +71,8 @@ SIGNATURES = {
     "tc_paged_rotate_keys": (_I, [_PP, _I, _I64P, _I, _I, _P, _I64, _I, _I, _I, _FP, _P]),
     "tc_prefill_attention": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _S, _I, _I64, _I64, _I, _I,
                                   _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
+    "tc_prefill_paged_attention": (_I, [_P, _I64P, _P, _P, _I64P, _I, _P, _I64, _P, _I64P, _P, _S, _I, _I64, _I64,
+                                        _I, _I, _I, _I, _I, _F, _I, _P, _S, _P, _I64P, _P]),
     "tc_prefill_num_splits": (_I, [_I, _I64, _I64, _I, _I]),
     "tc_prefill_workspace_bytes": (_S, [_I, _I64, _I, _I]),
     "tc_prefill_tiles_bytes": (_S, [_I64, _I64, _I, _I, _I]),

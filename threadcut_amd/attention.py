@@ -13,14 +13,15 @@ heads folded into a length-g query against the unexpanded cache. Prefill
 on the unexpanded K/V for GPU tensors in float16/bfloat16 with head_dim 128,
 g in (1, 2, 4, 8) and no mask or a boolean [b|1, 1, q, n] mask (what the
 registered ``sdpa_mask`` produces). Other prefill calls keep the reference's
-own path: expand KV once and run SDPA.
+own path: expand KV once and run SDPA. A paged cache (``paged.new_paged_cache``)
+hands over its page pools; its layers run the paged decode and prefill kernels.
 """
 import torch
 import torch.nn.functional as F
 from transformers import AttentionInterface
 from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 
-from . import kv, prefill
+from . import kv, paged, prefill
 from .flash_decode import decode_append_at, decode_append_into, decode_into, supports as decode_supports
 
 NAME = "threadcut"
@@ -41,9 +42,12 @@ def attention(module, query, key, value, attention_mask, dropout=0.0, scaling=No
     (views into the cache). Returns ([b, q, hq, d] contiguous, None).
     """
     b, hq, q, d = query.shape
+    scaling = scaling if scaling is not None else query.shape[-1] ** -0.5
+    layer = paged.layer_of(key)
+    if layer is not None:  # a paged cache layer handed over its pools
+        return paged.attention(layer, query, attention_mask, scaling), None
     hkv = key.shape[1]
     g = hq // hkv
-    scaling = scaling if scaling is not None else d ** -0.5
     if q == 1 and attention_mask is None and not decode_supports(query, key, value):
         # The reference's decode path for calls its GPU kernel does not serve
         # (attention.py:40-42): the g query heads of a KV head as a length-g query.

@@ -101,6 +101,14 @@ struct PartialArgs {
   const int32_t* tiles;
   int64_t max_tiles;
   int32_t pages, page_tokens;
+  // Paged append with device lengths (tok_off != null): sequence b holds
+  // lens[b] tokens before this step; tile entries carry their first logical
+  // position in the 4th word, and a tile's rows are those below lens[b]
+  // (tiles reserved ahead read nothing). The new token goes to logical
+  // position lens[b], whose row sits tok_off[b * tok_pitch + lens[b]] bytes
+  // into the head slab of the pools.
+  const int32_t* tok_off;
+  int64_t tok_pitch;
 };
 
 struct CombineArgs {
@@ -264,12 +272,16 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   int32_t len = len_cap;
   const int32_t* tab = nullptr;
   int32_t last_tile = -1;  // paged append: the tile whose last row is the new token's slot
+  int32_t plen = -1;  // paged append with device lengths: tokens cached before this step
   if constexpr (PAGED) {
     // Token index space of 16 per tile; a tile's own row count masks the rest.
     const int32_t ntiles = min(max(a.tiles[b], 0), static_cast<int32_t>(a.max_tiles));
     len = 16 * ntiles;
     tab = a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4;
-    if (a.k_new) last_tile = ntiles - 1;
+    if (a.tok_off)
+      plen = min(max(a.lens[b], 0), static_cast<int32_t>(a.tok_pitch) - 1);
+    else if (a.k_new)
+      last_tile = ntiles - 1;
   } else if (a.lens) {
     len = min(max(a.lens[b], 0), len_cap);
   }
@@ -302,6 +314,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (ti >> 4));
       e_page = e.x; e_slot = e.y;
       e_rows = (ti >> 4) == last_tile ? e.z - 1 : e.z;  // the new token is attended from k_new
+      if (plen >= 0) e_rows = min(e.z, max(plen - e.w, 0));
     }
   }
   int32_t li = 0;  // the wave's tiles loaded so far
@@ -316,7 +329,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
         const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (t0 >> 4));
         page = __builtin_amdgcn_readfirstlane(e.x);
         slot = __builtin_amdgcn_readfirstlane(e.y);
-        rows = __builtin_amdgcn_readfirstlane((t0 >> 4) == last_tile ? e.z - 1 : e.z);
+        int32_t r = (t0 >> 4) == last_tile ? e.z - 1 : e.z;
+        if (plen >= 0) r = min(e.z, max(plen - e.w, 0));
+        rows = __builtin_amdgcn_readfirstlane(r);
       }
       ++li;
       load_paged_tile(tl, kslab, vslab, row_k, row_v, a.sk_b * 2, a.sv_b * 2, a.pages, a.page_tokens, page, slot,
@@ -432,9 +447,18 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       const uint16_t* src = is_v ? a.v_new + b * a.svn_b + h * a.svn_h : a.k_new + b * a.skn_b + h * a.skn_h;
       uint16_t* dst = nullptr;
       if constexpr (PAGED) {
-        // The new token's slot is the last row of the sequence's last tile;
-        // an invalid entry (or no tile) writes nothing.
-        if (last_tile >= 0) {
+        // The new token's slot: with device lengths, the offset table's row of
+        // position lens[b] (an offset outside the pool writes nothing);
+        // otherwise the last row of the sequence's last tile (an invalid entry,
+        // or no tile, writes nothing).
+        if (plen >= 0) {
+          const int32_t off = a.tok_off[static_cast<int64_t>(b) * a.tok_pitch + plen];
+          const int64_t room = static_cast<int64_t>(a.pages) * a.sk_b * 2 - h * a.sk_h * 2 - kHeadDim * 2;
+          if (off >= 0 && off <= room) {
+            char* base = reinterpret_cast<char*>(is_v ? a.v_w + h * a.sv_h : a.k_w + h * a.sk_h);
+            dst = reinterpret_cast<uint16_t*>(base + off);
+          }
+        } else if (last_tile >= 0) {
           const int4 e = *reinterpret_cast<const int4*>(tab + 4 * last_tile);
           if (!(e.x < 0 || e.x >= a.pages || e.y < 0 || e.z < 1 || e.z > 16 || e.y > a.page_tokens - e.z)) {
             const int64_t slot = e.y + e.z - 1;
@@ -729,6 +753,8 @@ struct Paged {
   const int32_t* tiles;     // [B]
   int64_t max_tiles;
   int pages, page_tokens;
+  const int32_t* tok_off = nullptr;  // device-length append: [B, tok_pitch] row byte offsets
+  int64_t tok_pitch = 0;
 };
 
 int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
@@ -799,6 +825,8 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.max_tiles = paged ? paged->max_tiles : 0;
   a.pages = paged ? paged->pages : 0;
   a.page_tokens = paged ? paged->page_tokens : 0;
+  a.tok_off = paged ? paged->tok_off : nullptr;
+  a.tok_pitch = paged ? paged->tok_pitch : 0;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, s)
@@ -1071,6 +1099,44 @@ int tc_decode_paged_append_attention(const void* q_dev, const int64_t q_strides[
   const Append app{k_new_dev, k_new_strides, v_new_dev, v_new_strides, k_pool_dev, v_pool_dev};
   const Paged p{tile_table_dev, tiles_dev, max_tiles, num_pages, page_tokens};
   return attention_impl(q_dev, q_strides, k_pool_dev, pool_strides, v_pool_dev, pool_strides, nullptr,
+                        16 * max_tiles, batch, kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev,
+                        workspace_bytes, out_dev, out_strides, &app, batch > 1, stream, &p);
+}
+
+int tc_decode_paged_append_attention_at(const void* q_dev, const int64_t q_strides[3], void* k_pool_dev,
+                                        void* v_pool_dev, const int64_t pool_strides[3], int num_pages,
+                                        int page_tokens, const int32_t* tile_table_dev, const int32_t* tiles_dev,
+                                        int64_t max_tiles, const int32_t* tok_off_dev, int64_t tok_pitch,
+                                        const int32_t* lens_dev, const void* k_new_dev,
+                                        const int64_t k_new_strides[2], const void* v_new_dev,
+                                        const int64_t v_new_strides[2], int batch, int kv_heads, int group,
+                                        int head_dim, int dtype, float scale, int split_tokens, void* workspace_dev,
+                                        size_t workspace_bytes, void* out_dev, const int64_t out_strides[3],
+                                        void* stream) {
+  clear_error();
+  if (num_pages < 1 || page_tokens < 1)
+    return fail(TC_ERR_INVALID_ARGUMENT, "pool of %d pages of %d tokens", num_pages, page_tokens);
+  if (max_tiles < 1 || max_tiles > kMaxTokens / 16)
+    return fail(TC_ERR_INVALID_ARGUMENT, "append needs max_tiles in [1, %lld] (got %lld)",
+                (long long)(kMaxTokens / 16), (long long)max_tiles);
+  if (!tile_table_dev || !tiles_dev || !tok_off_dev || !lens_dev)
+    return fail(TC_ERR_INVALID_ARGUMENT, "null tile table, token offsets or lengths");
+  if (!aligned16(tile_table_dev)) return fail(TC_ERR_ALIGNMENT, "tile table not 16-byte aligned");
+  if (tok_pitch < 1 || tok_pitch > kMaxTokens)
+    return fail(TC_ERR_INVALID_ARGUMENT, "token offset rows of %lld entries", (long long)tok_pitch);
+  if (!pool_strides) return fail(TC_ERR_INVALID_ARGUMENT, "null pool strides");
+  if (static_cast<int64_t>(num_pages) * pool_strides[0] * 2 >= (int64_t(1) << 31))
+    return fail(TC_ERR_UNSUPPORTED, "pools of 2 GiB or more (token offsets are 32-bit)");
+  if (!k_new_dev || !v_new_dev || !k_new_strides || !v_new_strides)
+    return fail(TC_ERR_INVALID_ARGUMENT, "null new-token K/V");
+  if (!aligned16(k_new_dev) || !aligned16(v_new_dev))
+    return fail(TC_ERR_ALIGNMENT, "new-token K/V not 16-byte aligned");
+  for (int i = 0; i < 2; ++i)
+    if (k_new_strides[i] < 0 || v_new_strides[i] < 0 || k_new_strides[i] % 8 || v_new_strides[i] % 8)
+      return fail(TC_ERR_ALIGNMENT, "new-token K/V strides must be non-negative multiples of 8");
+  const Append app{k_new_dev, k_new_strides, v_new_dev, v_new_strides, k_pool_dev, v_pool_dev};
+  const Paged p{tile_table_dev, tiles_dev, max_tiles, num_pages, page_tokens, tok_off_dev, tok_pitch};
+  return attention_impl(q_dev, q_strides, k_pool_dev, pool_strides, v_pool_dev, pool_strides, lens_dev,
                         16 * max_tiles, batch, kv_heads, group, head_dim, dtype, scale, split_tokens, workspace_dev,
                         workspace_bytes, out_dev, out_strides, &app, batch > 1, stream, &p);
 }

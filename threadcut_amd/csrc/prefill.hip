@@ -95,6 +95,14 @@ struct PrefillArgs {
   int kv_heads, causal, neg, splits;
   int fold_cus;             // > 0: pair work items w and W-1-w on one CU (see the kernel), W <= 2 x this
   float c;                  // |scale| * log2(e)
+  // Paged K/V (prefill_kernel<DT, G, true>): k and v are page pools whose head
+  // slabs start at k + h * sk_h (v + h * sv_h); the row of sequence b's
+  // logical key t sits tok_off[b * tok_pitch + t] bytes into the slab (the
+  // same offset in K and V). pool_bytes_k / _v bound the buffer ranges from
+  // the slab start, so a wrong offset reads zeros, not another allocation.
+  const int32_t* tok_off;
+  int64_t tok_pitch;
+  int64_t pool_bytes_k, pool_bytes_v;
 };
 
 template <int DT> struct Mfma;
@@ -158,6 +166,25 @@ __device__ __forceinline__ void load_stage(Stage& s, const char* kslab, const ch
   }
 }
 
+// Paged: the same chunks, each row found through the byte offsets of the
+// tile's 64 keys, which every wave holds one per lane (idx: lane l has key
+// key0 + l, or kNoRow past the end, which reads zeros).
+constexpr int32_t kNoRow = INT32_MIN;  // as an unsigned offset, 2^31: past every buffer range
+__device__ __forceinline__ void load_stage_paged(Stage& s, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                                 int32_t idx) {
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kk = (lane >> 4) + 4 * (t >> 6) + 16 * i;     // key of K chunk t + 256 i
+    const int kv = 4 * ((lane >> 4) + 4 * (t >> 6)) + i;    // key of V row i
+    const int32_t ok = __builtin_amdgcn_ds_bpermute(4 * kk, idx);
+    const int32_t ov = __builtin_amdgcn_ds_bpermute(4 * kv, idx);
+    s.k[i] = bload(rk, ok + 16 * (t & 15));
+    s.v[i] = bload(rv, ov + 16 * (t & 15));
+  }
+}
+
 // K rows as they are; V transposed to V^T[dim][key] (4 keys x 8 dims per thread).
 __device__ __forceinline__ void store_stage(const Stage& s, uint16_t* lk, uint16_t* lv) {
   const int t = threadIdx.x;
@@ -205,7 +232,7 @@ template <> constexpr uint32_t kOnes<TC_DTYPE_BF16> = 0x3F803F80u;
 // Key offset (within a 32-key half) of accumulator v of a lane in half `hi`.
 __device__ __forceinline__ int acc_key(int v, int hi) { return 8 * (v >> 2) + 4 * hi + (v & 3); }
 
-template <int DT, int G>
+template <int DT, int G, bool PAGED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_WAVES, TC_PREFILL_WAVES))) void prefill_kernel(
     const PrefillArgs a) {
   constexpr int kTokens = kRows / G;   // query tokens per work-group
@@ -262,9 +289,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     }
   }
 
-  const char* kslab = reinterpret_cast<const char*>(a.k + b * a.sk_b + h * a.sk_h);
-  const char* vslab = reinterpret_cast<const char*>(a.v + b * a.sv_b + h * a.sv_h);
+  const char* kslab = reinterpret_cast<const char*>(a.k + (PAGED ? 0 : b * a.sk_b) + h * a.sk_h);
+  const char* vslab = reinterpret_cast<const char*>(a.v + (PAGED ? 0 : b * a.sv_b) + h * a.sv_h);
   const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
+  // Paged: buffer ranges over the pools from this head's slab on, and the
+  // offsets of a tile's 64 keys, one per lane (kNoRow past n).
+  const __amdgpu_buffer_rsrc_t prk = rsrc(kslab, PAGED ? static_cast<int32_t>(a.pool_bytes_k - h * a.sk_h * 2) : 0);
+  const __amdgpu_buffer_rsrc_t prv = rsrc(vslab, PAGED ? static_cast<int32_t>(a.pool_bytes_v - h * a.sv_h * 2) : 0);
+  const int32_t* toff = PAGED ? a.tok_off + b * a.tok_pitch : nullptr;
+  auto tile_rows = [&](int64_t tile) -> int32_t {
+    const int64_t key = tile * kKeys + lane;
+    return key < a.n ? toff[key] : kNoRow;
+  };
+  auto stage = [&](Stage& st_, int64_t tile, int32_t idx) {
+    if constexpr (PAGED)
+      load_stage_paged(st_, prk, prv, idx);
+    else
+      load_stage(st_, kslab, vslab, row_k, row_v, tile * kKeys, a.n);
+  };
   const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.pitch : nullptr;
 
   // Tiles this work-group may need: its split's share of all n keys, cut at
@@ -333,19 +375,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   int64_t t = next_active(t_begin);
   int cls_t = t < nt ? tile_class(t) : TILE_SKIP;
   if (t < nt) {
-    load_stage(st, kslab, vslab, row_k, row_v, t * kKeys, a.n);
+    int32_t rows_t = kNoRow;
+    if constexpr (PAGED) rows_t = tile_rows(t);
+    stage(st, t, rows_t);
     store_stage(st, s_k[0], s_v[0]);
   }
   int64_t tn = t < nt ? next_active(t + 1) : nt;
   int cls_n = tn < nt ? tile_class(tn) : TILE_SKIP;
+  // Paged: the row offsets of the tile loaded next, fetched one tile ahead.
+  int32_t rows_n = kNoRow;
+  if constexpr (PAGED) rows_n = tn < nt ? tile_rows(tn) : kNoRow;
   __syncthreads();
 
   int buf = 0;
   while (t < nt) {
     const bool more = tn < nt;
-    if (more) load_stage(st, kslab, vslab, row_k, row_v, tn * kKeys, a.n);
+    if (more) stage(st, tn, rows_n);
     const int64_t tnn = more ? next_active(tn + 1) : nt;
     const int cls_nn = tnn < nt ? tile_class(tnn) : TILE_SKIP;
+    if constexpr (PAGED) rows_n = tnn < nt ? tile_rows(tnn) : kNoRow;
     const int cls = cls_t;
     const uint16_t* lk = s_k[buf];
     const uint16_t* lv = s_v[buf];
@@ -605,15 +653,23 @@ __global__ __launch_bounds__(64) void mask_tiles_kernel(const uint8_t* mask, int
   }
 }
 
+template <int DT, bool PAGED>
+void launch_attention(const PrefillArgs& a, int group, dim3 grid, hipStream_t stream) {
+  switch (group) {
+    case 1: hipLaunchKernelGGL((prefill_kernel<DT, 1, PAGED>), grid, dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<DT, 2, PAGED>), grid, dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<DT, 4, PAGED>), grid, dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((prefill_kernel<DT, 8, PAGED>), grid, dim3(256), 0, stream, a); break;
+  }
+}
+
 template <int DT>
 hipError_t launch_dt(const PrefillArgs& a, int group, int batch, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(a.nblk * a.kv_heads * batch * a.splits));
-  switch (group) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<DT, 1>), grid, dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<DT, 2>), grid, dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<DT, 4>), grid, dim3(256), 0, stream, a); break;
-    default: hipLaunchKernelGGL((prefill_kernel<DT, 8>), grid, dim3(256), 0, stream, a); break;
-  }
+  if (a.tok_off)
+    launch_attention<DT, true>(a, group, grid, stream);
+  else
+    launch_attention<DT, false>(a, group, grid, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   const int hq_total = a.kv_heads * group;
@@ -759,15 +815,22 @@ extern "C" int tc_prefill_mask_tiles(const uint8_t* mask_dev, const int64_t mask
   return hip_status(hipGetLastError(), "mask tile launch");
 }
 
-extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3], const void* k_dev,
-                                    const int64_t k_strides[3], const void* v_dev, const int64_t v_strides[3],
-                                    const uint8_t* mask_dev, const int64_t mask_strides[3],
-                                    const uint8_t* mask_tiles_dev, size_t mask_tiles_bytes, int causal,
-                                    int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
-                                    int head_dim, int dtype, float scale, int num_splits, void* workspace_dev,
-                                    size_t workspace_bytes_in, void* out_dev, const int64_t out_strides[3],
-                                    void* stream) {
-  clear_error();
+namespace tc {
+namespace {
+
+// The page pools of a paged prefill call.
+struct PagedPools {
+  const int32_t* tok_off;  // [batch, tok_pitch] byte offsets of each logical key's row in its head slab
+  int64_t tok_pitch;
+  int64_t pool_bytes;      // bytes of one pool (K and V pools share the shape)
+};
+
+int prefill_impl(const void* q_dev, const int64_t q_strides[3], const void* k_dev, const int64_t k_strides[3],
+                 const void* v_dev, const int64_t v_strides[3], const uint8_t* mask_dev,
+                 const int64_t mask_strides[3], const uint8_t* mask_tiles_dev, size_t mask_tiles_bytes, int causal,
+                 int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads, int head_dim, int dtype,
+                 float scale, int num_splits, void* workspace_dev, size_t workspace_bytes_in, void* out_dev,
+                 const int64_t out_strides[3], void* stream, const PagedPools* pools) {
   int group = 0, rc;
   if (batch < 1 || batch > 65535) return fail(TC_ERR_INVALID_ARGUMENT, "batch %d", batch);
   if ((rc = check_group(q_heads, kv_heads, &group)) != TC_OK) return rc;
@@ -852,8 +915,56 @@ extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3
   }
   a.neg = scale < 0.f ? 1 : 0;
   a.c = static_cast<float>(std::fabs(static_cast<double>(scale)) * 1.4426950408889634);
+  a.tok_off = pools ? pools->tok_off : nullptr;
+  a.tok_pitch = pools ? pools->tok_pitch : 0;
+  a.pool_bytes_k = a.pool_bytes_v = pools ? pools->pool_bytes : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == TC_DTYPE_F16 ? launch_dt<TC_DTYPE_F16>(a, group, batch, s)
                                              : launch_dt<TC_DTYPE_BF16>(a, group, batch, s);
   return hip_status(e, "prefill launch");
+}
+
+}  // namespace
+}  // namespace tc
+
+extern "C" int tc_prefill_attention(const void* q_dev, const int64_t q_strides[3], const void* k_dev,
+                                    const int64_t k_strides[3], const void* v_dev, const int64_t v_strides[3],
+                                    const uint8_t* mask_dev, const int64_t mask_strides[3],
+                                    const uint8_t* mask_tiles_dev, size_t mask_tiles_bytes, int causal,
+                                    int64_t q_len, int64_t n_tokens, int batch, int q_heads, int kv_heads,
+                                    int head_dim, int dtype, float scale, int num_splits, void* workspace_dev,
+                                    size_t workspace_bytes_in, void* out_dev, const int64_t out_strides[3],
+                                    void* stream) {
+  clear_error();
+  return prefill_impl(q_dev, q_strides, k_dev, k_strides, v_dev, v_strides, mask_dev, mask_strides, mask_tiles_dev,
+                      mask_tiles_bytes, causal, q_len, n_tokens, batch, q_heads, kv_heads, head_dim, dtype, scale,
+                      num_splits, workspace_dev, workspace_bytes_in, out_dev, out_strides, stream, nullptr);
+}
+
+extern "C" int tc_prefill_paged_attention(const void* q_dev, const int64_t q_strides[3], const void* k_pool_dev,
+                                          const void* v_pool_dev, const int64_t pool_strides[3], int num_pages,
+                                          const int32_t* tok_off_dev, int64_t tok_pitch, const uint8_t* mask_dev,
+                                          const int64_t mask_strides[3], const uint8_t* mask_tiles_dev,
+                                          size_t mask_tiles_bytes, int causal, int64_t q_len, int64_t n_tokens,
+                                          int batch, int q_heads, int kv_heads, int head_dim, int dtype, float scale,
+                                          int num_splits, void* workspace_dev, size_t workspace_bytes_in,
+                                          void* out_dev, const int64_t out_strides[3], void* stream) {
+  clear_error();
+  if (!pool_strides) return fail(TC_ERR_INVALID_ARGUMENT, "null pool strides");
+  if (num_pages < 1) return fail(TC_ERR_INVALID_ARGUMENT, "pool of %d pages", num_pages);
+  if (q_len > 0 && (!tok_off_dev || tok_pitch < n_tokens))
+    return fail(TC_ERR_INVALID_ARGUMENT, "token offsets: null or a row of %lld for %lld keys", (long long)tok_pitch,
+                (long long)n_tokens);
+  if (reinterpret_cast<uintptr_t>(tok_off_dev) & 3u) return fail(TC_ERR_ALIGNMENT, "token offsets not 4-byte aligned");
+  // Rows are found by 32-bit byte offsets from a head's slab.
+  const int64_t pool_bytes = static_cast<int64_t>(num_pages) * pool_strides[0] * 2;
+  if (pool_strides[0] < 1 || pool_bytes >= (int64_t(1) << 31) ||
+      static_cast<int64_t>(kv_heads - 1) * pool_strides[1] * 2 >= pool_bytes)
+    return fail(TC_ERR_UNSUPPORTED, "pool of %lld bytes (page stride %lld): paged prefill needs a pool under 2 GiB",
+                (long long)pool_bytes, (long long)pool_strides[0]);
+  const PagedPools pools{tok_off_dev, tok_pitch, pool_bytes};
+  return prefill_impl(q_dev, q_strides, k_pool_dev, pool_strides, v_pool_dev, pool_strides, mask_dev, mask_strides,
+                      mask_tiles_dev, mask_tiles_bytes, causal, q_len, n_tokens, batch, q_heads, kv_heads, head_dim,
+                      dtype, scale, num_splits, workspace_dev, workspace_bytes_in, out_dev, out_strides, stream,
+                      &pools);
 }

@@ -19,53 +19,143 @@ the step passes transformers an already-prepared empty mask mapping: left to
 itself, transformers builds a mask tensor while a graph is being captured
 (and the attention call would then take the prefill branch).
 
-The host keeps each GrowingLayer's token count in step (``n``) so that the
-cache is an ordinary GrowingLayer cache again after ``close()``: splice,
-prefill and eager decode work on it as before.
+The host keeps each layer's token count in step (``n``) so that the cache is
+an ordinary cache again after ``close()``: splice, prefill and eager decode
+work on it as before.
+
+Two cache kinds are captured: ``kv.new_cache`` caches (GrowingLayer buffers,
+grown once to the step's capacity; the append position is a device counter)
+and ``paged.new_paged_cache`` caches (slots for the new tokens reserved ahead
+in the page table, whose tile table and token offsets are uploaded once; the
+sequence lengths are the device counter).
 """
 import torch
 
-from . import kv
+from . import kv, paged
 
 
-class DecodeGraph:
-    """Captured decode step of `model` (run with the "threadcut" attention) over `cache`.
+class _GrowingCache:
+    """The GrowingLayer cache of a DecodeGraph."""
 
-    cache: a ``kv.new_cache`` cache that has been prefilled (every layer holds
-    the same n tokens). Its buffers are grown once to hold `max_new_tokens`
-    more, then the step is captured. ``step(ids)`` feeds one token per
-    sequence and returns the logits [B, vocab] of that position (a static
-    tensor, overwritten by the next step). ``close()`` hands the cache back.
-    """
-
-    def __init__(self, model, cache, max_new_tokens, batch=1):
+    def __init__(self, cache, batch, max_new_tokens):
         layers = cache.layers
         if not layers or not all(isinstance(l, kv.GrowingLayer) and getattr(l, "kbuf", None) is not None
                                  for l in layers):
-            raise ValueError("DecodeGraph: needs a prefilled kv.new_cache() cache")
+            raise ValueError("DecodeGraph: needs a prefilled kv.new_cache() or paged.new_paged_cache() cache")
         n = layers[0].n
         if any(l.n != n for l in layers):
             raise ValueError("DecodeGraph: every layer must hold the same number of tokens")
         if layers[0].kbuf.shape[0] != batch:
             raise ValueError(f"DecodeGraph: cache batch {layers[0].kbuf.shape[0]} != {batch}")
-        types = set(getattr(model.config, "layer_types", None) or ["full_attention"])
-        if types != {"full_attention"}:
-            raise ValueError(f"DecodeGraph: layer types {sorted(types)}; only full-attention models are captured")
-        dev = layers[0].kbuf.device
-        self.model, self.cache, self.layers, self.batch = model, cache, layers, batch
+        self.layers = layers
         for l in layers:
             l.flush()
             l._reserve(n + max_new_tokens + 1, l.kbuf)
             l._view()
+        self.device = layers[0].kbuf.device
         self.capacity = layers[0].kbuf.shape[-2]
         # The captured kernels hold these buffers' addresses: keep the tensors, and check
         # before every replay that each layer still uses them.
         self.buffers = [(l.kbuf, l.vbuf) for l in layers]
+
+    def attach(self, pos):
+        for l in self.layers:
+            l.device_pos = pos
+
+    def in_step(self, flag):
+        for l in self.layers:
+            l.in_graph_step = flag
+
+    def advance(self, k):
+        for l in self.layers:
+            l.n += k
+            l._view()
+
+    def unchanged(self, n, pos):
+        return all(l.kbuf is kb and l.vbuf is vb and l.n == n and l.device_pos is pos
+                   for l, (kb, vb) in zip(self.layers, self.buffers))
+
+    def detach(self):
+        for l in self.layers:
+            l.device_pos = None
+            l.pending = None
+            l._view()
+
+
+class _PagedCache:
+    """The paged cache of a DecodeGraph: max_new_tokens + 1 slots per sequence reserved in
+    the page table up front, the tables uploaded once, the unused slots released on close."""
+
+    def __init__(self, cache, batch, max_new_tokens):
+        self.state = state = paged.state_of(cache)
+        if state.kv is None:
+            raise ValueError("DecodeGraph: the paged cache holds no tokens yet")
+        table = state.kv.table
+        self.layers = layers = cache.layers
+        for l in layers:
+            l.flush()
+        n = layers[0].n
+        if any(l.n != n for l in layers) or any(table.length(b) != n for b in range(table.batch)):
+            raise ValueError("DecodeGraph: every layer and sequence of the paged cache must hold the same tokens")
+        if table.batch != batch:
+            raise ValueError(f"DecodeGraph: cache batch {table.batch} != {batch}")
+        for b in range(batch):
+            table.reserve(b, max_new_tokens + 1)
+        self.device = state.kv.device
+        self.capacity = n + max_new_tokens + 1
+        # Uploaded once here; the captured kernels read these tensors on every replay.
+        self.tables = (state.kv.device_table(), state.kv.device_offsets())
+        self.version = table.version
+
+    def attach(self, pos):
+        self.state.device_lens = pos
+
+    def in_step(self, flag):
+        self.state.in_graph_step = flag
+
+    def advance(self, k):
+        for l in self.layers:
+            l.n += k
+
+    def unchanged(self, n, pos):
+        return (self.state.kv.table.version == self.version and self.state.device_lens is pos
+                and all(l.n == n for l in self.layers))
+
+    def detach(self):
+        self.state.device_lens = None
+        for l in self.layers:
+            l.pending = None
+        n = self.layers[0].n
+        table = self.state.kv.table
+        for b in range(table.batch):
+            table.prune(b, n, table.length(b), 0)
+
+
+class DecodeGraph:
+    """Captured decode step of `model` (run with the "threadcut" attention) over `cache`.
+
+    cache: a prefilled ``kv.new_cache`` or ``paged.new_paged_cache`` cache
+    (every layer holding the same n tokens), with room made once for
+    `max_new_tokens` more; then the step is captured. ``step(ids)`` feeds one
+    token per sequence and returns the logits [B, vocab] of that position (a
+    static tensor, overwritten by the next step). ``close()`` hands the cache
+    back.
+    """
+
+    def __init__(self, model, cache, max_new_tokens, batch=1):
+        types = set(getattr(model.config, "layer_types", None) or ["full_attention"])
+        if types != {"full_attention"}:
+            raise ValueError(f"DecodeGraph: layer types {sorted(types)}; only full-attention models are captured")
+        self.store = (_PagedCache if paged.state_of(cache) is not None else _GrowingCache)(cache, batch,
+                                                                                          max_new_tokens)
+        dev = self.store.device
+        self.model, self.cache, self.layers, self.batch = model, cache, cache.layers, batch
+        self.capacity = self.store.capacity
+        n = self.layers[0].n
         self.pos = torch.full((batch,), n, dtype=torch.int32, device=dev)
         self.position_ids = torch.full((batch, 1), n, dtype=torch.long, device=dev)
         self.ids = torch.zeros((batch, 1), dtype=torch.long, device=dev)
-        for l in layers:
-            l.device_pos = self.pos
+        self.store.attach(self.pos)
 
         # Warm-up on a side stream (library loading, allocator pools), then undo its token.
         side = torch.cuda.Stream(device=dev)
@@ -79,22 +169,19 @@ class DecodeGraph:
         with torch.cuda.graph(self.graph):
             self.logits = self._step_body()
         # Capture ran the Python once and no kernel: take back the host-side count.
-        for l in self.layers:
-            l.n -= 1
+        self.store.advance(-1)
 
     @torch.no_grad()
     def _step_body(self):
         # One new token per sequence sees every cached token: no mask. Handing the
         # (empty) mask mapping over keeps transformers from building a mask tensor,
         # which it does while a graph is being captured.
-        for l in self.layers:
-            l.in_graph_step = True
+        self.store.in_step(True)
         try:
             out = self.model(input_ids=self.ids, position_ids=self.position_ids, past_key_values=self.cache,
                              attention_mask={"full_attention": None}, use_cache=True, logits_to_keep=1)
         finally:
-            for l in self.layers:
-                l.in_graph_step = False
+            self.store.in_step(False)
         logits = out.logits[:, -1]
         self.pos.add_(1)
         self.position_ids.add_(1)
@@ -103,9 +190,7 @@ class DecodeGraph:
     def _rewind(self):
         self.pos.sub_(1)
         self.position_ids.sub_(1)
-        for l in self.layers:
-            l.n -= 1
-            l._view()
+        self.store.advance(-1)
 
     @property
     def n(self):
@@ -119,20 +204,17 @@ class DecodeGraph:
         n = self.layers[0].n
         if n + 1 > self.capacity:
             raise RuntimeError(f"DecodeGraph: the cache holds {self.capacity} tokens; close() and grow it")
-        for l, (kb, vb) in zip(self.layers, self.buffers):
-            if l.kbuf is not kb or l.vbuf is not vb or l.n != n or l.device_pos is not self.pos:
-                raise RuntimeError("DecodeGraph: the cache changed outside the graph since capture")
+        if not self.store.unchanged(n, self.pos):
+            raise RuntimeError("DecodeGraph: the cache changed outside the graph since capture")
         self.ids.copy_(torch.as_tensor(ids).reshape(self.batch, 1), non_blocking=True)
         self.graph.replay()
-        for l in self.layers:
-            l.n += 1
+        self.store.advance(1)
         return self.logits
 
     def close(self):
-        """Return the layers to host-counted operation (views refreshed)."""
+        """Return the layers to host-counted operation (views refreshed, reserved slots freed)."""
+        if self.graph is None:
+            return
         torch.cuda.current_stream(self.pos.device).synchronize()
-        for l in self.layers:
-            l.device_pos = None
-            l.pending = None
-            l._view()
+        self.store.detach()
         self.graph = None

@@ -156,7 +156,23 @@ def _group_by_layout(layers):
 
 
 def splice(cache, s, inv_freq):
-    """Rewrite every layer of a DynamicCache from A·B·C·(tail) to A·C (threadcut/kv.py:28-41)."""
+    """Rewrite every layer of a DynamicCache from A·B·C·(tail) to A·C (threadcut/kv.py:28-41).
+
+    A paged cache (paged.new_paged_cache) is pruned instead: the pages of the dropped span
+    go back to the free list and the kept suffix's keys are re-rotated where they are."""
+    from . import paged
+
+    state = paged.state_of(cache)
+    if state is not None:
+        state.check_not_captured("splice")
+        for layer in cache.layers:
+            layer.flush()
+        if state.kv is not None:
+            for b in range(state.batch):
+                state.kv.prune(b, s, inv_freq)
+        for layer in cache.layers:
+            layer.n = s.a + s.c
+        return
     if all(isinstance(layer, GrowingLayer) for layer in cache.layers):
         live = [layer for layer in cache.layers if getattr(layer, "kbuf", None) is not None]
         for layer in live:

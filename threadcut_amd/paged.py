@@ -26,6 +26,9 @@ frees pages and C needs only a key re-rotation. This module is that cache:
 """
 import numpy as np
 import torch
+import torch.nn.functional as F
+from transformers import DynamicCache
+from transformers.cache_utils import DynamicLayer
 
 from . import _lib
 from .flash_decode import HEAD_DIM, num_splits
@@ -164,15 +167,31 @@ class PageTable:
         return np.stack([fr[rep, 0], fr[rep, 1] + i], axis=1)
 
     def tile_table(self):
-        """int32 [B, max_tiles, 4] and tiles int32 [B] (numpy)."""
+        """int32 [B, max_tiles, 4] and tiles int32 [B] (numpy): entries {page, first slot,
+        rows, first logical position} in logical order."""
         per = [tiles_of(f) for f in self.frags]
         mt = max(1, max(len(t) for t in per))
         tab = np.zeros((self.batch, mt, 4), dtype=np.int32)
         cnt = np.zeros(self.batch, dtype=np.int32)
         for b, ts in enumerate(per):
             tab[b, :len(ts), :3] = ts
+            tab[b, :len(ts), 3] = np.cumsum(ts[:, 2]) - ts[:, 2]
             cnt[b] = len(ts)
         return tab, cnt
+
+    def token_offsets(self, page_bytes, slot_bytes, pitch=None):
+        """int32 [B, pitch]: byte offset of every logical token's row within a head slab of
+        the pools (page * page_bytes + slot * slot_bytes); past a sequence's end, INT32_MIN,
+        which no buffer range covers."""
+        n = max([self.length(b) for b in range(self.batch)] + [1])
+        pitch = max(n, int(pitch or 0))
+        off = np.full((self.batch, pitch), np.iinfo(np.int32).min, dtype=np.int64)
+        for b in range(self.batch):
+            sl = self.token_slots(b)
+            off[b, :len(sl)] = sl[:, 0] * page_bytes + sl[:, 1] * slot_bytes
+        if off.max() >= 2 ** 31:
+            raise RuntimeError("PageTable.token_offsets: pools of 2 GiB or more need 64-bit offsets")
+        return off.astype(np.int32)
 
 
 class PagedKV:
@@ -247,6 +266,70 @@ class PagedKV:
             self._dev_table = (ver, torch.from_numpy(tab).to(self.device), torch.from_numpy(cnt).to(self.device),
                                tab.shape[1])
         return self._dev_table[1:]
+
+    def device_offsets(self):
+        """(token offsets int32 [B, pitch], pitch) on the device: the byte offset of each logical
+        token's row in a head slab of the pools (PageTable.token_offsets), for the paged prefill
+        and the device-length decode step."""
+        ver = self.table.version
+        if getattr(self, "_dev_off", None) is None or self._dev_off[0] != ver:
+            st = self.k_pools[0].stride()
+            off = self.table.token_offsets(st[0] * 2, st[2] * 2)
+            self._dev_off = (ver, torch.from_numpy(off).to(self.device), off.shape[1])
+        return self._dev_off[1:]
+
+    def prefill(self, layer, query, scale, mask=None, causal=False, out=None):
+        """The prefill branch of threadcut/attention.py:43-46 over the pools: query
+        [B, Hq, q, D] (any strides, last dim contiguous) attends the first n keys of every
+        sequence (n = the sequences' common length; the last q of them are the queries'
+        own tokens), in logical order, with no mask, is_causal, or a boolean mask
+        [B|1, 1, q, n]. Returns [B, q, Hq, D] (the reference's transposed output)."""
+        from . import prefill as pf
+
+        self._refuse_during_step("prefill")
+        _lib.require_gpu(query, what="PagedKV.prefill")
+        b, hq, ql, d = query.shape
+        lens = {self.table.length(i) for i in range(self.table.batch)}
+        if b != self.table.batch or d != HEAD_DIM or query.dtype != self.dtype or query.device != self.device:
+            raise ValueError(f"PagedKV.prefill: query {tuple(query.shape)} {query.dtype} does not fit the cache")
+        if len(lens) != 1:
+            raise ValueError(f"PagedKV.prefill: sequences of different lengths {sorted(lens)}")
+        n = lens.pop()
+        if not 0 <= ql <= n or hq % self.kv_heads:
+            raise ValueError(f"PagedKV.prefill: {ql} queries over {n} keys, {hq} query heads")
+        if out is None:
+            out = torch.empty((b, ql, hq, d), dtype=query.dtype, device=query.device)
+        if ql == 0:
+            return out
+        if mask is not None and causal:
+            raise ValueError("PagedKV.prefill: pass either a mask or causal")
+        off, pitch = self.device_offsets()
+        tiles, tiles_bytes, mptr, mst = None, 0, None, _lib.i64x3(0, 0, 1)
+        if mask is not None:
+            m = mask
+            if m.dtype != torch.bool or m.dim() != 4 or m.shape[1] != 1 or m.shape[0] not in (1, b) \
+                    or tuple(m.shape[2:]) != (ql, n) or m.device != self.device:
+                raise ValueError(f"PagedKV.prefill: the mask must be bool [B|1, 1, {ql}, {n}] on the pools' device")
+            if m.stride(3) != 1 and n > 1:  # the kernel reads mask rows as contiguous bytes
+                m = m.contiguous()
+            tiles = pf.mask_tiles(m, hq, self.kv_heads)
+            tiles_bytes = tiles.numel()
+            m = m[:, 0]
+            mptr, mst = m.data_ptr(), pf._mask_strides(m)
+        lib = _lib.load()
+        kp, vp = self.k_pools[layer], self.v_pools[layer]
+        with torch.cuda.device(self.device):
+            splits = pf.num_splits(b, ql, n, hq, self.kv_heads)
+            nbytes = lib.tc_prefill_workspace_bytes(b, ql, hq, splits)
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+            rc = lib.tc_prefill_paged_attention(
+                query.data_ptr(), pf._strides(query, (0, 1, 2)), kp.data_ptr(), vp.data_ptr(), self._strides(),
+                kp.shape[0], off.data_ptr(), pitch, mptr, mst,
+                None if tiles is None else tiles.data_ptr(), tiles_bytes, int(bool(causal)), ql, n, b, hq,
+                self.kv_heads, d, _lib.dtype_code(self.dtype), float(scale), splits, ws.data_ptr(), ws.numel(),
+                out.data_ptr(), pf._strides(out, (0, 1, 2)), _lib.stream_of(self.device))
+            _lib.check(rc, "tc_prefill_paged_attention")
+        return out
 
     def _step_pending(self):
         """True between reserve_step() and the last layer's decode_append of that step:
@@ -374,6 +457,40 @@ class PagedKV:
         step[1].discard(layer)
         return out
 
+    def decode_append_at(self, layer, q, k_new, v_new, lens, scale, out=None):
+        """decode_append with the sequence lengths on the device (int32 [B], tokens before the
+        step), for a captured step: the new rows go to logical positions lens[b], whose slots
+        must already be in the table (reserved ahead), and q attends positions [0, lens[b]].
+        Nothing here reads lens on the host, so a graph of this call stays valid while lens
+        advances; the table must not change meanwhile."""
+        b, hkv, g, d = q.shape
+        kn = k_new.reshape(b, hkv, HEAD_DIM)
+        vn = v_new.reshape(b, hkv, HEAD_DIM)
+        for name, t in (("q", q), ("k_new", kn), ("v_new", vn)):
+            if t.stride(-1) != 1 or t.dtype != self.dtype or t.device != self.device:
+                raise ValueError(f"PagedKV.decode_append_at: {name} must be {self.dtype} on {self.device}, "
+                                 "last dim contiguous")
+        if lens.dtype != torch.int32 or lens.shape != (b,) or lens.device != self.device:
+            raise ValueError("PagedKV.decode_append_at: lens must be int32 [B] on the pools' device")
+        if out is None:
+            out = torch.empty_like(q)
+        tab, cnt, mt = self.device_table()
+        off, pitch = self.device_offsets()
+        lib = _lib.load()
+        kp, vp = self.k_pools[layer], self.v_pools[layer]
+        with torch.cuda.device(self.device):
+            s = num_splits(b, hkv, TILE * mt, None, ragged=b > 1)
+            nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
+            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+            rc = lib.tc_decode_paged_append_attention_at(
+                q.data_ptr(), _lib.i64x3(*q.stride()[:3]), kp.data_ptr(), vp.data_ptr(), self._strides(),
+                kp.shape[0], kp.shape[2], tab.data_ptr(), cnt.data_ptr(), mt, off.data_ptr(), pitch, lens.data_ptr(),
+                kn.data_ptr(), _lib.i64x2(kn.stride(0), kn.stride(1)), vn.data_ptr(),
+                _lib.i64x2(vn.stride(0), vn.stride(1)), b, hkv, g, d, _lib.dtype_code(self.dtype), float(scale), 0,
+                ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.i64x3(*out.stride()[:3]), _lib.stream_of(self.device))
+            _lib.check(rc, "tc_decode_paged_append_attention_at")
+        return out
+
     def prune(self, b, s, inv_freq):
         """Keep tokens [0, s.a) and [s.c0, s.c0 + s.c) of sequence b (a threadcut
         Split): the dropped span's pages are freed and the kept suffix's keys are
@@ -397,3 +514,179 @@ class PagedKV:
                                               _lib.stream_of(self.device))
                 _lib.check(rc, "tc_paged_rotate_keys")
         return freed
+
+
+# ---------------------------------------------------------------------------
+# The paged cache behind transformers' cache interface.
+# ---------------------------------------------------------------------------
+
+# PagedLayers by the address of their K pool: update() returns the pools, and
+# the "threadcut" attention finds the layer behind them here.
+_LAYERS = {}
+
+
+def layer_of(key):
+    """The PagedLayer whose K pool `key` is, or None."""
+    if not isinstance(key, torch.Tensor) or not key.is_cuda:
+        return None
+    layer = _LAYERS.get(key.data_ptr())
+    if layer is None or layer.owner.kv is None or layer.owner.kv.k_pools[layer.index] is not key:
+        return None
+    return layer
+
+
+class PagedCacheState:
+    """What the layers of one paged cache share: the PagedKV (made at the first update,
+    when the head count, dtype and device are known), the fused-append switch and, while
+    a DecodeGraph holds the cache, the device lengths of its captured step."""
+
+    def __init__(self, num_layers, num_pages, page_tokens, batch, fused_append):
+        self.num_layers, self.num_pages, self.page_tokens, self.batch = num_layers, num_pages, page_tokens, batch
+        self.fused_append = fused_append
+        self.kv = None
+        self.layers = []
+        self.device_lens = None
+        self.in_graph_step = False
+
+    def ensure_pools(self, like):
+        if self.kv is None:
+            if like.dim() != 4 or like.shape[0] != self.batch or like.shape[-1] != HEAD_DIM:
+                raise ValueError(f"paged cache: K/V {tuple(like.shape)} for a batch of {self.batch} at head_dim "
+                                 f"{HEAD_DIM}")
+            self.kv = PagedKV(self.num_layers, like.shape[1], self.num_pages, self.page_tokens, batch=self.batch,
+                              dtype=like.dtype, device=like.device)
+
+    def check_not_captured(self, what):
+        if self.device_lens is not None and not self.in_graph_step:
+            raise RuntimeError(f"paged cache {what}: a DecodeGraph holds this cache; close() it first")
+
+    def write(self, layer, keys, values):
+        """Rows of positions [layer.n, layer.n + add) of every sequence into the layer's pools,
+        reserving the slots when this is the first layer to reach them."""
+        kv = self.kv
+        add = keys.shape[-2]
+        need = layer.n + add - kv.table.length(0)
+        if need > 0:
+            for b in range(self.batch):
+                kv.table.reserve(b, need)
+        kp, vp = kv.k_pools[layer.index], kv.v_pools[layer.index]
+        for b in range(self.batch):
+            sl = torch.from_numpy(kv.table.token_slots(b)[layer.n:layer.n + add]).to(kv.device)
+            kp[sl[:, 0], :, sl[:, 1]] = keys[b].transpose(0, 1).to(kv.dtype)
+            vp[sl[:, 0], :, sl[:, 1]] = values[b].transpose(0, 1).to(kv.dtype)
+
+    def reserve_step_for(self, layer):
+        """A decode step's slot per sequence: reserved by the first layer of the step."""
+        if layer.n == self.kv.table.length(0):
+            self.kv.reserve_step()
+
+
+class PagedLayer(DynamicLayer):
+    """A transformers cache layer whose K/V rows live in the pools of a PagedKV shared by
+    every layer of the cache (one page table for all).
+
+    update() writes the new tokens' rows into their slots and returns the layer's K and V
+    pools, which the "threadcut" attention recognises (layer_of) and serves with the paged
+    kernels: decode over the tile table, prefill through the token offsets. With
+    fused_append a one-token update reserves the step's slot and leaves the row pending;
+    the decode kernel writes it while it attends.
+    """
+
+    def __init__(self, owner, index):
+        super().__init__()
+        self.owner, self.index = owner, index
+        self.n = 0
+        self.pending = None
+
+    @property
+    def kv(self):
+        return self.owner.kv
+
+    def lazy_initialization(self, key_states, value_states):
+        super().lazy_initialization(key_states, value_states)
+        self.owner.ensure_pools(key_states)
+        self.n = 0
+
+    def flush(self):
+        """Write a pending row that no attention call consumed."""
+        if self.pending is not None:
+            k, v = self.pending
+            self.pending = None
+            if self.owner.device_lens is None:
+                self.kv.write_step(self.index, k, v)
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        self.owner.check_not_captured("update")
+        self.flush()
+        add = key_states.shape[-2]
+        if add == 1 and self.owner.device_lens is not None:
+            self.pending = (key_states, value_states)  # written at lens[b] by the captured kernel
+        elif add == 1 and self.owner.fused_append and key_states.is_cuda:
+            self.owner.reserve_step_for(self)
+            self.pending = (key_states, value_states)
+        else:
+            self.owner.write(self, key_states, value_states)
+        self.n += add
+        kp = self.kv.k_pools[self.index]
+        _LAYERS[kp.data_ptr()] = self
+        return kp, self.kv.v_pools[self.index]
+
+    def get_seq_length(self):
+        return self.n if self.is_initialized else 0
+
+    def crop(self, max_length):
+        raise NotImplementedError("PagedLayer.crop: shorten a paged cache with kv.splice (a prune) instead")
+
+
+def new_paged_cache(config, num_pages, page_tokens=64, batch=1, fused_append=True):
+    """A DynamicCache whose layers keep their K/V in page pools (PagedKV): the engine's
+    cache (threadcut/kv.py:95-98) in the layout the reference's README.md:141-144 proposes.
+    Use it with the "threadcut" attention; kv.splice prunes it (pages of the dropped span
+    freed, the kept suffix's keys re-rotated in place)."""
+    cache = DynamicCache(config=config)
+    state = PagedCacheState(len(cache.layers), num_pages, page_tokens, batch, fused_append)
+    cache.layers = [PagedLayer(state, i) for i in range(len(cache.layers))]
+    state.layers = cache.layers
+    return cache
+
+
+def state_of(cache):
+    """The PagedCacheState of a new_paged_cache() cache, or None."""
+    layers = getattr(cache, "layers", None)
+    if layers and all(isinstance(l, PagedLayer) for l in layers):
+        return layers[0].owner
+    return None
+
+
+def attention(layer, query, attention_mask, scaling):
+    """The "threadcut" attention for a paged layer: query [B, Hq, q, D] -> [B, q, Hq, D]."""
+    b, hq, q, d = query.shape
+    kv = layer.kv
+    hkv = kv.kv_heads
+    g = hq // hkv
+    if q == 1 and attention_mask is None:
+        out = torch.empty((b, 1, hq, d), dtype=query.dtype, device=query.device)
+        qg, og = query.reshape(b, hkv, g, d), out.view(b, hkv, g, d)
+        if layer.pending is not None:
+            k_new, v_new = layer.pending
+            layer.pending = None
+            if layer.owner.device_lens is not None:
+                kv.decode_append_at(layer.index, qg, k_new, v_new, layer.owner.device_lens, scaling, out=og)
+            else:
+                kv.decode_append(layer.index, qg, k_new, v_new, scaling, out=og)
+        else:
+            kv.decode(layer.index, qg, scaling, out=og)
+        return out
+    layer.flush()
+    is_causal = attention_mask is None and q > 1 and q == layer.n
+    m = attention_mask
+    if m is None or (m.dtype == torch.bool and m.dim() == 4 and m.shape[1] == 1):
+        return kv.prefill(layer.index, query, scaling, m, is_causal)
+    # Other masks: the reference's route (repeat_kv + SDPA) on the gathered keys.
+    ks, vs = zip(*[kv.gather(layer.index, i) for i in range(b)])
+    k, v = torch.stack(ks), torch.stack(vs)
+    out = F.scaled_dot_product_attention(query, k.repeat_interleave(g, 1), v.repeat_interleave(g, 1),
+                                         attn_mask=m, scale=scaling, is_causal=is_causal)
+    return out.transpose(1, 2).contiguous()
