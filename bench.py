@@ -491,7 +491,7 @@ def measure_decode_step(dev, n=10240, steps=40):
     import torch
     from transformers import AutoModelForCausalLM, Qwen3Config
 
-    from threadcut_amd import attention, kv
+    from threadcut_amd import attention, kv, paged
     from threadcut_amd.graph import DecodeGraph
 
     torch.manual_seed(8)
@@ -530,12 +530,29 @@ def measure_decode_step(dev, n=10240, steps=40):
         torch.cuda.synchronize()
         graph_ms = (time.perf_counter() - t0) * 1e3 / steps
         dg.close()
+        del caches, dg
+        # The same step over the paged cache (64-token pages), prefilled the same way.
+        pcache = paged.new_paged_cache(cfg, num_pages=n // 64 + steps // 64 + 8, page_tokens=64)
+        for i in range(0, n, 2048):
+            model(input_ids=prompt[:, i:i + 2048], past_key_values=pcache, use_cache=True, logits_to_keep=1)
+        pg = DecodeGraph(model, pcache, max_new_tokens=steps + 8)
+        for _ in range(3):
+            pg.step(tok)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            pg.step(tok)
+        torch.cuda.synchronize()
+        paged_ms = (time.perf_counter() - t0) * 1e3 / steps
+        pg.close()
+        del pcache, pg
     weights = sum(p.numel() * p.element_size() for p in model.parameters())
-    del model, caches, dg
+    del model
     torch.cuda.empty_cache()
     return {"kv_tokens": n, "layers": LAYERS, "weights_GB": round(weights / 1e9, 2),
             "eager_ms_per_token": round(eager_ms, 3), "graph_ms_per_token": round(graph_ms, 3),
             "speedup": round(eager_ms / graph_ms, 2),
+            "graph_ms_per_token_paged_cache": round(paged_ms, 3),
             "graph_weight_read_GB/s": round(weights / (graph_ms * 1e-3) / 1e9, 1),
             "note": "random-init weights; the step includes every layer's projections, MLP and the LM head"}
 
@@ -692,7 +709,46 @@ def measure_paged(dev, n, steps, page_tokens=64):
         "pages_freed": len(freed), "host_us_bookkeeping": round(host_us, 1)}
     del cache, td
     torch.cuda.empty_cache()
+    out["prefill_chunk_2048_on_7716"] = measure_paged_prefill(dev, page_tokens)
     return out
+
+
+def measure_paged_prefill(dev, page_tokens, iters=10):
+    """The engine's prefill chunk (2048 queries over 7716 cached keys, bool causal mask, Qwen3-4B
+    heads, fp16) through the page pools (per-token row offsets, pages from a shuffled free list)
+    against the contiguous prefill kernel on the same keys gathered into one buffer."""
+    import random
+
+    import torch
+
+    from threadcut_amd import prefill, workloads
+    from threadcut_amd.paged import PagedKV
+
+    L, n = workloads.PREFILL_CHUNK, workloads.PREFILL_PAST + workloads.PREFILL_CHUNK
+    q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, device=dev)
+    mask = workloads.causal_mask(L, n, device=dev)
+    cache = PagedKV(1, HKV, -(-n // page_tokens) + 4, page_tokens, device=dev)
+    random.Random(9).shuffle(cache.table.free)
+    cache.append(0, [k[0]], [v[0]])
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters * 1e3
+
+    us_paged = timed(lambda: cache.prefill(0, q, D ** -0.5, mask))
+    us_contig = timed(lambda: prefill.prefill_attention(q, k, v, mask, D ** -0.5))
+    tflops = prefill_flops(L, n, True) / (us_paged * 1e-6) / 1e12
+    del cache, q, k, v, mask
+    torch.cuda.empty_cache()
+    return {"page_tokens": page_tokens, "us_per_call": round(us_paged, 1), "tflops": round(tflops, 1),
+            "contiguous_us_per_call": round(us_contig, 1)}
 
 
 def measure_match(seconds=2.0):
