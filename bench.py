@@ -212,35 +212,48 @@ def bench_splice(dev, steps, warmup):
     import torch
 
     from threadcut_amd import _lib, kv, workloads
+    from threadcut_amd.match import Split
 
     s = workloads.SPLICE_SPLIT
     n = workloads.SPLICE_TOKENS
     ks, vs = workloads.layer_caches(1, LAYERS, n, device=dev)
-    table = _lib.float_array(kv.rope_table(-s.gap, workloads.inv_freq(1e6)))
     lib = _lib.load()
     kp = _lib.ptr_array([t.data_ptr() for t in ks])
     vp = _lib.ptr_array([t.data_ptr() for t in vs])
     st = _lib.i64x3(*ks[0].stride()[:3])
 
-    def run():
-        # The same move every time: the buffers' contents change, the work does not.
-        _lib.check(lib.tc_splice_rope(kp, vp, LAYERS, st, 1, HKV, n, D, _lib.TC_DTYPE_F16, s.a, s.c0, s.c,
-                                      table, _lib.stream_of(dev)), "tc_splice_rope")
+    def timed(sp, reps, warm):
+        tab = _lib.float_array(kv.rope_table(-sp.gap, workloads.inv_freq(1e6)))
 
-    for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+        def run():
+            # The same move every time: the buffers' contents change, the work does not.
+            _lib.check(lib.tc_splice_rope(kp, vp, LAYERS, st, 1, HKV, n, D, _lib.TC_DTYPE_F16, sp.a, sp.c0, sp.c,
+                                          tab, _lib.stream_of(dev)), "tc_splice_rope")
+
+        for _ in range(warm):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    ms = timed(s, steps, warmup)
     gbs = splice_bytes(s.c) / (ms * 1e-3) / 1e9
+    # Overlapping moves whose gap is under 48 rows (the row walk), 12188 rows per strip.
+    short = {}
+    for gap in (1, 17, 32, 47):
+        sp = Split(2048, 2048 + gap, 12188)
+        t = timed(sp, max(4, steps // 10), 2)
+        g = splice_bytes(sp.c) / (t * 1e-3) / 1e9
+        short[str(gap)] = {"us_per_splice": round(t * 1e3, 1), "GB/s": round(g, 1), "frac": round(g / PEAK_GBS, 4)}
     return {"us_per_splice": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
             "bytes": splice_bytes(s.c), "config": {"layers": LAYERS, "tokens": n, "split": [s.a, s.c0, s.c],
-                                                   "theta": 1e6}}
+                                                   "theta": 1e6},
+            "short_gap_walk": {"split": "Split(2048, 2048 + gap, 12188)", "by_gap": short}}
 
 
 SWEEP = (1536, 4096, 10240, 14336)

@@ -12,6 +12,8 @@
 // stored with no intermediate buffer; V rows take the same path unrotated.
 // 8 threads cover a row, a pass of 256 threads covers 32 rows, and a thread
 // keeps kUnroll passes of loads in flight before it stores.
+#include <algorithm>
+
 #include "tc_common.hpp"
 
 namespace tc {
@@ -38,6 +40,23 @@ constexpr int kMaxJobs = 128;                      // strips sets per launch (64
 // (splice_kernel with DEPTH > 0); shorter gaps walk each strip in row order
 // with one work-group. Chains win from about two work-groups per strip.
 constexpr int64_t kChainMin = TC_SPLICE_CHAIN_MIN;
+// An overlapping move with a shorter gap walks each strip in row order, cut
+// into up to this many segments of at least kWalkMinRows rows that one
+// work-group walks together (splice_walk_kernel). 36 layers x 12188 rows:
+// two segments 727-769 us across gaps 1-47, against 760-780 us for one walk
+// per strip; three, four and eight segments, or two rows per thread and
+// pass, are slower (more concurrent streams or bytes in flight cost more than
+// they hide).
+#ifndef TC_SPLICE_WALK_SEGMENTS
+#define TC_SPLICE_WALK_SEGMENTS 2
+#endif
+#ifndef TC_SPLICE_WALK_MIN_ROWS
+#define TC_SPLICE_WALK_MIN_ROWS 256
+#endif
+constexpr int kWalkSegments = TC_SPLICE_WALK_SEGMENTS;
+constexpr int64_t kWalkMinRows = TC_SPLICE_WALK_MIN_ROWS;
+static_assert(kWalkSegments == 1 || kWalkSegments == 2 || kWalkSegments == 4 || kWalkSegments == 8,
+              "walk segments: 1, 2, 4 or 8");
 // Chain rows a thread loads before it stores them: 8 holds a whole chain of up
 // to 8 rows at 128 VGPRs; longer chains run faster with 16 (235 VGPRs) in
 // flight, shorter ones slower (occupancy).
@@ -59,8 +78,11 @@ struct SpliceArgs {
   int64_t src_row0, dst_row0, rows;
   int heads;
   int rot_jobs;    // jobs [0, rot_jobs) are keys (rotated), the rest copied
-  int sequential;  // 1: one work-group walks a whole strip in row order
   int64_t chain;   // > 0: chain walk of a move whose gap (src_row0 - dst_row0) is chain
+  // Row walk (splice_walk_kernel): segments of seg_rows rows (a multiple of
+  // the pass), the last one shorter; gap = src_row0 - dst_row0 < rows.
+  int segments;
+  int64_t seg_rows;
 };
 
 __device__ __forceinline__ uint4 load16(const uint16_t* p) {
@@ -164,8 +186,8 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
     return;
   }
 
-  int64_t row = a.sequential ? 0 : static_cast<int64_t>(blockIdx.x) * kTileRows;
-  const int64_t row_end = a.sequential ? a.rows : min(row + kTileRows, a.rows);
+  int64_t row = static_cast<int64_t>(blockIdx.x) * kTileRows;
+  const int64_t row_end = min(row + kTileRows, a.rows);
   for (; row < row_end; row += kTileRows) {
     uint4 lo[kUnroll], hi[kUnroll];
 #pragma unroll
@@ -177,12 +199,6 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
         hi[i] = load16(p + kHalf);
       }
     }
-    if (a.sequential) {
-      // Sources of this tile may be destinations of the same tile (gap < tile)
-      // and of the next one: every load of the tile lands before any store.
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-    }
 #pragma unroll
     for (int i = 0; i < kUnroll; ++i) {
       const int64_t r = row + i * kRowsPerPass + r_in;
@@ -191,6 +207,84 @@ __global__ __launch_bounds__(kThreads) void splice_kernel(const SpliceArgs a) {
         uint16_t* p = dst + (a.dst_row0 + r) * a.ds_t;
         store16(p, lo[i]);
         store16(p + kHalf, hi[i]);
+      }
+    }
+  }
+}
+
+// Overlapping move with a short gap, one work-group per strip. Destination
+// row r takes source row r + gap. The strip's rows are cut into segments of
+// seg_rows rows, walked together in row order, one 32-row pass of every
+// segment at a time: every load of a pass lands before any store of it (a
+// pass's sources reach gap rows into its own destinations), and the next
+// pass's sources lie past this pass's destinations. A segment's last gap
+// source rows are the next segment's first gap destination rows, which that
+// segment overwrites in its first pass: they are copied to LDS (the halo)
+// before any store and read from there.
+template <int DT, int SEG>
+__global__ __launch_bounds__(kThreads) void splice_walk_kernel(const SpliceArgs a) {
+  extern __shared__ uint4 halo[];  // [(segments - 1) * gap rows][16 chunks]
+  const int job = blockIdx.z;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.heads;
+  const int64_t h = bh % a.heads;
+  const bool rot = job < a.rot_jobs;
+  const int r_in = threadIdx.x >> 3;
+  const int u = threadIdx.x & 7;
+  const int64_t gap = a.src_row0 - a.dst_row0;
+  const int64_t L = a.seg_rows;
+  const int segs = a.segments;
+
+  const uint16_t* src_strip = a.src[job] + b * a.ss_b + h * a.ss_h;
+  const uint16_t* src = src_strip + 8 * u;
+  uint16_t* dst = a.dst[job] + b * a.ds_b + h * a.ds_h + 8 * u;
+
+  float cv[8], sv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cv[i] = a.cs[8 * u + i];
+    sv[i] = a.cs[kHalf + 8 * u + i];
+  }
+
+  // Halo k, row j: source row (k + 1) L - gap + j of segment k.
+  const int64_t halo_chunks = (segs - 1) * gap * 8;
+  for (int64_t i = threadIdx.x; i < halo_chunks; i += kThreads) {
+    const int64_t k = i / (gap * 8);
+    const int64_t j = (i >> 3) - k * gap;
+    const int uu = static_cast<int>(i & 7);
+    const uint16_t* p = src_strip + (a.src_row0 + (k + 1) * L - gap + j) * a.ss_t + 8 * uu;
+    halo[(k * gap + j) * 16 + uu] = load16(p);
+    halo[(k * gap + j) * 16 + 8 + uu] = load16(p + kHalf);
+  }
+  __syncthreads();
+
+  for (int64_t off = 0; off < L; off += kRowsPerPass) {
+    uint4 lo[SEG], hi[SEG];
+#pragma unroll
+    for (int k = 0; k < SEG; ++k) {
+      const int64_t r = k * L + off + r_in;
+      if (k < segs && r < min((k + 1) * L, a.rows)) {
+        const int64_t j = r - ((k + 1) * L - gap);
+        if (k < segs - 1 && j >= 0) {
+          lo[k] = halo[(k * gap + j) * 16 + u];
+          hi[k] = halo[(k * gap + j) * 16 + 8 + u];
+        } else {
+          const uint16_t* p = src + (a.src_row0 + r) * a.ss_t;
+          lo[k] = load16(p);
+          hi[k] = load16(p + kHalf);
+        }
+      }
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SEG; ++k) {
+      const int64_t r = k * L + off + r_in;
+      if (k < segs && r < min((k + 1) * L, a.rows)) {
+        if (rot) rotate_pair<DT>(lo[k], hi[k], cv, sv);
+        uint16_t* p = dst + (a.dst_row0 + r) * a.ds_t;
+        store16(p, lo[k]);
+        store16(p + kHalf, hi[k]);
       }
     }
   }
@@ -264,6 +358,14 @@ int check_ptrs(const char* what, void* const* ptrs, int n) {
   return TC_OK;
 }
 
+template <int SEG>
+void launch_walk(bool f16, dim3 grid, unsigned lds, hipStream_t stream, const SpliceArgs& a) {
+  if (f16)
+    hipLaunchKernelGGL((splice_walk_kernel<TC_DTYPE_F16, SEG>), grid, dim3(kThreads), lds, stream, a);
+  else
+    hipLaunchKernelGGL((splice_walk_kernel<TC_DTYPE_BF16, SEG>), grid, dim3(kThreads), lds, stream, a);
+}
+
 template <int DEPTH>
 void launch_kernel(bool f16, dim3 grid, hipStream_t stream, const SpliceArgs& a) {
   const unsigned lds = DEPTH > 0 ? 0 : kRowKernelLds;
@@ -302,8 +404,9 @@ int launch_rows(void* const* ksrc, void* const* vsrc, void* const* kdst, void* c
     a.rows = rows;
     a.heads = heads;
     a.rot_jobs = rotate ? nl : 0;
-    a.sequential = sequential ? 1 : 0;
     a.chain = chain;
+    a.segments = 1;
+    a.seg_rows = rows;
     const int64_t tiles = chain > 0 ? ceil_div(min(chain, rows), kRowsPerPass)
                                     : sequential ? 1 : ceil_div(rows, kTileRows);
     if (tiles > 0x7fffffff) return fail(TC_ERR_INVALID_ARGUMENT, "too many rows (%lld)", (long long)rows);
@@ -311,7 +414,23 @@ int launch_rows(void* const* ksrc, void* const* vsrc, void* const* kdst, void* c
                     static_cast<unsigned>(per_layer * nl));
     const int depth = chain <= 0 ? 0 : rows > kChainDepthShort * chain ? kChainDepthLong : kChainDepthShort;
     const bool f16 = dtype == TC_DTYPE_F16;
-    if (depth == kChainDepthLong)
+    if (sequential) {
+      // Segments of at least kWalkMinRows rows (and at least the gap, so a
+      // halo lies in its own segment's sources), a whole number of passes.
+      const int64_t gap = src_row0 - dst_row0;
+      if (gap <= 0 || gap >= rows || gap >= kChainMin)
+        return fail(TC_ERR_INVALID_ARGUMENT, "row walk of gap %lld over %lld rows", (long long)gap, (long long)rows);
+      const int64_t want = std::max<int64_t>(1, std::min<int64_t>(kWalkSegments, ceil_div(rows, kWalkMinRows)));
+      int64_t L = ceil_div(ceil_div(rows, want), kRowsPerPass) * kRowsPerPass;
+      L = std::max(L, ceil_div(gap, kRowsPerPass) * kRowsPerPass);
+      a.seg_rows = L;
+      a.segments = static_cast<int>(ceil_div(rows, L));
+      const unsigned lds = static_cast<unsigned>((a.segments - 1) * gap * kHeadDim * 2);
+      if (a.segments <= 1)
+        launch_walk<1>(f16, grid, lds, stream, a);
+      else
+        launch_walk<kWalkSegments>(f16, grid, lds, stream, a);
+    } else if (depth == kChainDepthLong)
       launch_kernel<kChainDepthLong>(f16, grid, stream, a);
     else if (depth == kChainDepthShort)
       launch_kernel<kChainDepthShort>(f16, grid, stream, a);
@@ -372,7 +491,7 @@ int tc_splice_rope(void* const* k_layers_host, void* const* v_layers_host, int n
   if (gap >= c)  // disjoint ranges: every row in parallel
     return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
                        batch, heads, dtype, c0, a, c, true, false, cos_sin_host, s);
-  if (gap < kChainMin)  // overlapping, short gap: one work-group walks each strip in row order
+  if (gap < kChainMin)  // overlapping, short gap: one work-group walks each strip in row order, in segments
     return launch_rows(k_layers_host, v_layers_host, k_layers_host, v_layers_host, num_layers, strides, strides,
                        batch, heads, dtype, c0, a, c, true, true, cos_sin_host, s);
   // Overlapping: gap independent chains per strip.
