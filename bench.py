@@ -460,13 +460,19 @@ def measure_prefill(dev, steps, only_case=None):
              ("prompt_2048_causal", 2048, 2048, False)]
     if only_case is not None:
         # One workload alone (for counter runs); "nomask_2048_on_9764" is the chunk shape without a mask.
-        cases = [c for c in cases + [("nomask_2048_on_9764", 2048, 9764, None)] if c[0] == only_case]
+        cases = [c for c in cases + [("nomask_2048_on_9764", 2048, 9764, None),
+                                     ("holes_2048_on_9764", 2048, 9764, "holes")] if c[0] == only_case]
         if not cases:
             raise SystemExit(f"unknown prefill case {only_case}")
     out = {}
     for name, L, n, masked in cases:
         q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, device=dev)
         mask = workloads.causal_mask(L, n, device=dev) if masked else None
+        if masked == "holes":
+            # Causal with one key in ten hidden at random: every active tile is
+            # tested per element against the mask bytes.
+            holes = torch.rand(L, n, generator=torch.Generator(device=dev).manual_seed(11), device=dev) < 0.1
+            mask = mask & ~holes[None, None]
         causal = masked is False
         scale = D ** -0.5
         iters = max(5, steps // 10)
@@ -477,7 +483,8 @@ def measure_prefill(dev, steps, only_case=None):
             is_causal=causal).transpose(1, 2).contiguous(), iters)
         tflops = prefill_flops(L, n, masked is not None) / (us * 1e-6) / 1e12
         r = {"q_len": L, "kv_tokens": n,
-             "mask": {True: "bool [1,1,q,n] causal", False: "is_causal", None: "none"}[masked],
+             "mask": {True: "bool [1,1,q,n] causal", False: "is_causal", None: "none",
+                      "holes": "bool [1,1,q,n] causal, 10% of keys hidden at random"}[masked],
              "splits": prefill.num_splits(1, L, n, HQ, HKV), "us_per_call": round(us, 1),
              "tflops": round(tflops, 1), "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16, 4),
              "reference_route_us": round(ref, 1), "speedup": round(ref / us, 2)}

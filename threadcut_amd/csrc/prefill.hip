@@ -441,17 +441,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
         int64_t lim64 = a.n - key0;
         if (a.causal || cls == TILE_CAUSAL) lim64 = min(lim64, past + tok[rg] + 1 - key0);
         const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
-        const uint8_t* mt = (cls == TILE_MIXED && mrow[rg]) ? mrow[rg] + key0 : nullptr;
         vis = 0;
+        if (cls == TILE_MIXED && mrow[rg]) {
+          // The row's 32 mask bytes of the tile as one batch of loads (one
+          // wait, no branch per key): keys at or past lim load the last
+          // visible key's byte (key 0 when none is), which stays inside the
+          // row, and the key < lim test hides them.
+          const uint8_t* mt = mrow[rg] + key0;
+          const int last = lim > 0 ? lim - 1 : 0;
+          uint8_t mb[32];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int key = 32 * kt + acc_key(v, hi);
-            bool ok = key < lim;
-            if (mt && ok) ok = mt[key] != 0;
-            vis |= ok ? (1u << (16 * kt + v)) : 0u;
-          }
+            for (int v = 0; v < 16; ++v) mb[16 * kt + v] = mt[min(32 * kt + acc_key(v, hi), last)];
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int key = 32 * kt + acc_key(v, hi);
+              vis |= (key < lim && mb[16 * kt + v] != 0) ? (1u << (16 * kt + v)) : 0u;
+            }
+        } else {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) vis |= 32 * kt + acc_key(v, hi) < lim ? (1u << (16 * kt + v)) : 0u;
+        }
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
