@@ -270,12 +270,15 @@ def summarize(r, nbytes):
 
 
 def stream_read_lib():
-    """The measurement library (threadcut_amd/csrc/bench): the streaming-read yardstick."""
+    """The measurement library (threadcut_amd/csrc/bench): the streaming-read yardstick of
+    the decode and the matrix-core ceiling of the prefill."""
     import ctypes
 
     from threadcut_amd import build
 
     lib = ctypes.CDLL(build.BENCH_LIB)
+    lib.tc_bench_mfma_ceiling.restype = ctypes.c_int
+    lib.tc_bench_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.tc_bench_stream_read.restype = ctypes.c_int
     lib.tc_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
                                          ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -436,6 +439,38 @@ def prefill_flops(q_len, n, causal_like, hq=HQ, d=D):
     return 4 * pairs * d * hq
 
 
+def measure_mfma_ceiling(dev, iters=2000):
+    """Back-to-back 32x32x16 fp16 MFMAs at the prefill's occupancy (two 256-thread
+    work-groups per CU), with constant and with random operand bits: PFLOP/s."""
+    import torch
+
+    lib = stream_read_lib()
+    wgs = 2 * torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(wgs * 256, dtype=torch.float32, device=dev)
+    out = {}
+    for name, rnd in (("constant_operands_pflops", 0), ("random_operands_pflops", 1)):
+        def run():
+            if lib.tc_bench_mfma_ceiling(rnd, wgs, iters, sink.data_ptr(), _stream(dev)):
+                raise RuntimeError("tc_bench_mfma_ceiling failed")
+        run()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(3):
+            run()
+        b.record()
+        torch.cuda.synchronize()
+        sec = a.elapsed_time(b) / 3 * 1e-3
+        out[name] = round(wgs * 4 * iters * 16 * 32768 / sec / 1e15, 3)
+    return out
+
+
+def _stream(dev):
+    from threadcut_amd import _lib
+
+    return _lib.stream_of(dev)
+
+
 def measure_prefill(dev, steps, only_case=None):
     """Prefill attention at the Qwen3-4B shape (32 q / 8 kv heads, D=128, fp16): the
     GQA-native kernel vs the reference's GPU route (repeat_kv + SDPA with the same mask)."""
@@ -495,6 +530,14 @@ def measure_prefill(dev, steps, only_case=None):
         out[name] = r
         del q, k, v, mask
     torch.cuda.empty_cache()
+    if only_case is None:
+        # What the matrix core sustains on data like these (its clock drops under
+        # toggling operands), and each workload against it.
+        ceil = measure_mfma_ceiling(dev)
+        for r in out.values():
+            r["frac_of_random_operand_ceiling"] = round(r["tflops"] / 1e3 / ceil["random_operands_pflops"], 4)
+        out["mfma_ceiling"] = {**ceil, "what": "v_mfma_f32_32x32x16_f16 back to back, 8 accumulators per wave, "
+                                              "two 256-thread work-groups per CU (libthreadcut_bench.so)"}
     return out
 
 
