@@ -427,6 +427,42 @@ int tc_prefill_mask_tiles(const uint8_t* mask, const int64_t mask_strides[3], in
 int tc_match_split(const int64_t* cached, int64_t n_cached, const int64_t* fresh, int64_t n_fresh,
                    int64_t min_suffix, int suffix, int64_t out[3]);
 
+/* ------------------------------------------------------------------------ */
+/* Page tables of the paged cache (host code, no GPU)                        */
+/* ------------------------------------------------------------------------ */
+
+/* The paged cache is this library's own (threadcut/README.md:141-144 proposes
+ * it; threadcut/kv.py:28-41,83-92 is the move it replaces): no reference
+ * function has these signatures. A sequence is a list of fragments, rows of
+ * int64 {page, first slot, count} in logical order (count >= 1 consecutive
+ * slots of one page).
+ *
+ * Tile entries {page, first slot, rows, logical start} of the fragments, each
+ * cut at multiples of 16 slots (the tile table of tc_decode_paged_attention,
+ * the tile list of tc_paged_rotate_keys); the first fragment starts at
+ * logical position first_pos. Returns the number of entries and writes them
+ * only when max_tiles is at least that (tiles may be NULL to ask), or
+ * -TC_ERR_INVALID_ARGUMENT for a malformed fragment. */
+int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t first_pos, int32_t* tiles, int64_t max_tiles);
+
+/* Prune of one sequence: keep logical tokens [0, a) and [c0, c0 + c). kept
+ * (room for num_frags + 1 rows) receives the new fragment list, the two kept
+ * ranges joined (their pieces merge when they are adjacent slots of one
+ * page); suffix (num_frags rows) the fragments of [c0, c0 + c) alone; freed
+ * (num_frags entries) the pages no kept fragment uses, ascending.
+ * counts = {kept rows, suffix rows, freed pages}. */
+int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t a, int64_t c0, int64_t c, int64_t* kept,
+                  int64_t* suffix, int64_t* freed, int64_t counts[3]);
+
+/* Byte offset of every logical token's row in a head slab of the pools,
+ * page * page_bytes + slot * slot_bytes, for the tokens of the fragments, and
+ * INT32_MIN (past every buffer range) up to pitch (the per-token offsets of
+ * tc_prefill_paged_attention and tc_decode_paged_append_attention_at).
+ * Returns the token count, or -TC_ERR_INVALID_ARGUMENT when it exceeds pitch,
+ * a fragment is malformed or an offset passes 2^31 - 1. */
+int64_t tc_page_token_offsets(const int64_t* frags, int64_t num_frags, int64_t page_bytes, int64_t slot_bytes,
+                              int32_t* out, int64_t pitch);
+
 #ifdef __cplusplus
 }
 #endif

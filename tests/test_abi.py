@@ -14,7 +14,7 @@ HEADER = os.path.join(ROOT, "include", "threadcut_hip.h")
 
 def declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int|size_t)\s+(tc_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|int64_t|size_t)\s+(tc_\w+)\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")

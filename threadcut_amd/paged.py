@@ -15,15 +15,19 @@ frees pages and C needs only a key re-rotation. This module is that cache:
   page. A prune cuts the list at the dropped span. A page no fragment uses any
   more goes back to the free list, and the kept fragments stay where they are.
 - Decode reads a tile table: each fragment is cut into tiles of at most 16
-  slots, entries ``{page, first slot, rows, 0}``
+  slots, entries ``{page, first slot, rows, first logical position}``
   (``tc_decode_paged_attention``). Attention over a set of keys does not
   depend on their order, so holes left by prunes cost nothing.
 - The prune's only device work is ``tc_paged_rotate_keys``: C's keys rotated
   in place by -(c0 - a) positions with the reference's rotation
   (threadcut/kv.py:20-25), for every layer in one launch. V is not touched.
 
-``PageTable`` is the bookkeeping alone (no device), ``PagedKV`` adds the pools.
+``PageTable`` is the bookkeeping alone (no device; its fragment arithmetic is the
+host code of ``tc_page_tiles``, ``tc_page_prune`` and ``tc_page_token_offsets``),
+``PagedKV`` adds the pools.
 """
+import ctypes
+
 import numpy as np
 import torch
 import torch.nn.functional as F
@@ -35,6 +39,7 @@ from .flash_decode import HEAD_DIM, num_splits
 from .kv import rope_table
 
 TILE = 16  # rows per tile-table entry (the decode kernel's tile)
+_I64P = ctypes.POINTER(ctypes.c_int64)
 
 
 _EMPTY = np.zeros((0, 3), dtype=np.int64)
@@ -61,21 +66,43 @@ def _cut(frags, lo, hi):
     return sub
 
 
+def _to_device(arr, device):
+    """A host numpy array as a device tensor: staged in pinned memory and copied on the
+    current stream without a host wait (torch keeps the staging block until the copy ran)."""
+    return torch.from_numpy(np.ascontiguousarray(arr)).pin_memory().to(device, non_blocking=True)
+
+
+def _addr(a):
+    return a.__array_interface__["data"][0]
+
+
+def _frag_arg(frags):
+    f = frags
+    if not (isinstance(f, np.ndarray) and f.dtype == np.int64 and f.ndim == 2 and f.flags.c_contiguous):
+        f = np.ascontiguousarray(np.asarray(frags, dtype=np.int64).reshape(-1, 3))
+    return f, _addr(f), len(f)
+
+
+def _tiles(frags, first_pos=0):
+    """Tile entries {page, first slot, rows, logical start} of a fragment array,
+    int32 [T, 4] (tc_page_tiles): each fragment cut at multiples of 16 slots."""
+    lib = _lib.load()
+    f, fp, nf = _frag_arg(frags)
+    n = lib.tc_page_tiles(fp, nf, int(first_pos), None, 0)
+    if n < 0:
+        _lib.check(-n, "tc_page_tiles")
+    out = np.empty((n, 4), dtype=np.int32)
+    if n:
+        _lib.check(0 if lib.tc_page_tiles(fp, nf, int(first_pos), _addr(out), n) == n
+                   else _lib.TC_ERR_INVALID_ARGUMENT, "tc_page_tiles")
+    return out
+
+
 def tiles_of(frags):
     """Tile entries (page, first slot, rows) of a fragment array, int32 [T, 3]:
     each fragment is cut at multiples of 16 slots, so full tiles are 16-slot
     aligned."""
-    frags = np.asarray(frags, dtype=np.int64).reshape(-1, 3)
-    if len(frags) == 0:
-        return np.zeros((0, 3), dtype=np.int32)
-    start, end = frags[:, 1], frags[:, 1] + frags[:, 2]
-    t0 = start // TILE
-    nt = (end - 1) // TILE + 1 - t0
-    rep = np.repeat(np.arange(len(frags)), nt)
-    k = np.arange(int(nt.sum())) - np.repeat(np.cumsum(nt) - nt, nt)
-    lo = np.maximum(start[rep], (t0[rep] + k) * TILE)
-    hi = np.minimum(end[rep], (t0[rep] + k + 1) * TILE)
-    return np.stack([frags[rep, 0], lo, hi - lo], axis=1).astype(np.int32)
+    return np.ascontiguousarray(_tiles(frags)[:, :3])
 
 
 class PageTable:
@@ -131,25 +158,24 @@ class PageTable:
 
     def prune(self, b, a, c0, c):
         """Keep tokens [0, a) and [c0, c0 + c) of sequence b; returns (the kept
-        suffix's fragments, the pages freed)."""
+        suffix's fragments, the pages freed) (tc_page_prune)."""
         old = self.frags[b]
         n = self.length(b)
         if not (0 <= a <= c0 and c >= 0 and c0 + c <= n):
             raise ValueError(f"prune: split (a={a}, c0={c0}, c={c}) outside a sequence of {n} tokens")
-        suffix = _cut(old, c0, c0 + c)
-        head = _cut(old, 0, a)
-        if len(head) and len(suffix) and head[-1, 0] == suffix[0, 0] and head[-1, 1] + head[-1, 2] == suffix[0, 1]:
-            # Adjacent pieces of one page merge back (a == c0 leaves the list as it was).
-            joint = head[-1:].copy()
-            joint[0, 2] += suffix[0, 2]
-            new = np.concatenate([head[:-1], joint, suffix[1:]])
-        else:
-            new = np.concatenate([head, suffix])
-        freed = sorted(set(old[:, 0].tolist()) - set(new[:, 0].tolist()))
-        self.frags[b] = new
+        f, fp, nf = _frag_arg(old)
+        # One buffer: kept (nf + 1 rows), suffix (nf rows), freed (nf), counts (3).
+        buf = np.empty(7 * nf + 6, dtype=np.int64)
+        base = _addr(buf)
+        rc = _lib.load().tc_page_prune(fp, nf, int(a), int(c0), int(c), base, base + 8 * (3 * nf + 3),
+                                       base + 8 * (6 * nf + 3), ctypes.cast(base + 8 * (7 * nf + 3), _I64P))
+        _lib.check(rc, "tc_page_prune")
+        nk, ns, nfr = (int(x) for x in buf[7 * nf + 3:])
+        self.frags[b] = buf[:3 * nk].reshape(nk, 3).copy()
+        freed = buf[6 * nf + 3:6 * nf + 3 + nfr].tolist()
         self.free += freed[::-1]
         self.version += 1
-        return suffix, freed
+        return buf[3 * nf + 3:3 * nf + 3 + 3 * ns].reshape(ns, 3).copy(), freed
 
     def release(self, b):
         """Drop sequence b entirely (its pages return to the free list)."""
@@ -169,13 +195,12 @@ class PageTable:
     def tile_table(self):
         """int32 [B, max_tiles, 4] and tiles int32 [B] (numpy): entries {page, first slot,
         rows, first logical position} in logical order."""
-        per = [tiles_of(f) for f in self.frags]
+        per = [_tiles(f) for f in self.frags]
         mt = max(1, max(len(t) for t in per))
         tab = np.zeros((self.batch, mt, 4), dtype=np.int32)
         cnt = np.zeros(self.batch, dtype=np.int32)
         for b, ts in enumerate(per):
-            tab[b, :len(ts), :3] = ts
-            tab[b, :len(ts), 3] = np.cumsum(ts[:, 2]) - ts[:, 2]
+            tab[b, :len(ts)] = ts
             cnt[b] = len(ts)
         return tab, cnt
 
@@ -185,13 +210,13 @@ class PageTable:
         which no buffer range covers."""
         n = max([self.length(b) for b in range(self.batch)] + [1])
         pitch = max(n, int(pitch or 0))
-        off = np.full((self.batch, pitch), np.iinfo(np.int32).min, dtype=np.int64)
+        off = np.empty((self.batch, pitch), dtype=np.int32)
+        lib = _lib.load()
         for b in range(self.batch):
-            sl = self.token_slots(b)
-            off[b, :len(sl)] = sl[:, 0] * page_bytes + sl[:, 1] * slot_bytes
-        if off.max() >= 2 ** 31:
-            raise RuntimeError("PageTable.token_offsets: pools of 2 GiB or more need 64-bit offsets")
-        return off.astype(np.int32)
+            f, fp, nf = _frag_arg(self.frags[b])
+            if lib.tc_page_token_offsets(fp, nf, int(page_bytes), int(slot_bytes), _addr(off[b]), pitch) < 0:
+                raise RuntimeError("PageTable.token_offsets: pools of 2 GiB or more need 64-bit offsets")
+        return off
 
 
 class PagedKV:
@@ -239,7 +264,7 @@ class PagedKV:
         slots = self.table.reserve(b, n)
         if n == 0:
             return
-        idx = torch.from_numpy(slots).to(self.device)
+        idx = _to_device(slots, self.device)
         pages, sl = idx[:, 0], idx[:, 1]
         for kp, vp, k, v in zip(self.k_pools, self.v_pools, ks, vs):
             k = k.reshape(self.kv_heads, n, HEAD_DIM)
@@ -253,7 +278,7 @@ class PagedKV:
         if len(slots) == 0:
             z = torch.empty(self.kv_heads, 0, HEAD_DIM, dtype=self.dtype, device=self.device)
             return z, z.clone()
-        idx = torch.from_numpy(slots).to(self.device)
+        idx = _to_device(slots, self.device)
         k = self.k_pools[layer][idx[:, 0], :, idx[:, 1]].transpose(0, 1).contiguous()
         v = self.v_pools[layer][idx[:, 0], :, idx[:, 1]].transpose(0, 1).contiguous()
         return k, v
@@ -263,7 +288,7 @@ class PagedKV:
         ver = self.table.version
         if self._dev_table is None or self._dev_table[0] != ver:
             tab, cnt = self.table.tile_table()
-            self._dev_table = (ver, torch.from_numpy(tab).to(self.device), torch.from_numpy(cnt).to(self.device),
+            self._dev_table = (ver, _to_device(tab, self.device), _to_device(cnt, self.device),
                                tab.shape[1])
         return self._dev_table[1:]
 
@@ -275,7 +300,7 @@ class PagedKV:
         if getattr(self, "_dev_off", None) is None or self._dev_off[0] != ver:
             st = self.k_pools[0].stride()
             off = self.table.token_offsets(st[0] * 2, st[2] * 2)
-            self._dev_off = (ver, torch.from_numpy(off).to(self.device), off.shape[1])
+            self._dev_off = (ver, _to_device(off, self.device), off.shape[1])
         return self._dev_off[1:]
 
     def prefill(self, layer, query, scale, mask=None, causal=False, out=None):
@@ -503,7 +528,7 @@ class PagedKV:
         if gap and len(tiles):
             t = np.zeros((len(tiles), 4), dtype=np.int32)
             t[:, :3] = tiles
-            td = torch.from_numpy(t).to(self.device)
+            td = _to_device(t, self.device)
             table = _lib.float_array(rope_table(-gap, inv_freq))
             lib = _lib.load()
             kp = _lib.ptr_array([p.data_ptr() for p in self.k_pools])
@@ -547,6 +572,7 @@ class PagedCacheState:
         self.layers = []
         self.device_lens = None
         self.in_graph_step = False
+        self._slots = {}
 
     def ensure_pools(self, like):
         if self.kv is None:
@@ -571,9 +597,20 @@ class PagedCacheState:
                 kv.table.reserve(b, need)
         kp, vp = kv.k_pools[layer.index], kv.v_pools[layer.index]
         for b in range(self.batch):
-            sl = torch.from_numpy(kv.table.token_slots(b)[layer.n:layer.n + add]).to(kv.device)
+            sl = self.slots_on_device(b, layer.n, layer.n + add)
             kp[sl[:, 0], :, sl[:, 1]] = keys[b].transpose(0, 1).to(kv.dtype)
             vp[sl[:, 0], :, sl[:, 1]] = values[b].transpose(0, 1).to(kv.dtype)
+
+    def slots_on_device(self, b, lo, hi):
+        """(page, slot) of sequence b's positions [lo, hi) on the device; every layer of a
+        step writes the same positions, so the upload is kept for the table version."""
+        key = (self.kv.table.version, b, lo, hi)
+        hit = self._slots.get(key)
+        if hit is None:
+            if self._slots and next(iter(self._slots))[0] != key[0]:
+                self._slots.clear()
+            hit = self._slots[key] = _to_device(self.kv.table.token_slots(b)[lo:hi], self.kv.device)
+        return hit
 
     def reserve_step_for(self, layer):
         """A decode step's slot per sequence: reserved by the first layer of the step."""
