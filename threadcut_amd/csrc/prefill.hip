@@ -93,6 +93,7 @@ struct PrefillArgs {
   float* o_part;            // splits > 1: [b, splits, L, hq, d] fp32, normalized per split
   float* lse_part;          // splits > 1: [b, splits, L, hq] log2-sum-exp of the split (-inf if empty)
   int kv_heads, causal, neg, splits;
+  int mask_words;           // mask rows 4-byte aligned: a tile's mask bytes load as words
   int fold_cus;             // > 0: pair work items w and W-1-w on one CU (see the kernel), W <= 2 x this
   float c;                  // |scale| * log2(e)
   // Paged K/V (prefill_kernel<DT, G, true>): k and v are page pools whose head
@@ -443,23 +444,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
         const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
         vis = 0;
         if (cls == TILE_MIXED && mrow[rg]) {
-          // The row's 32 mask bytes of the tile as one batch of loads (one
-          // wait, no branch per key): keys at or past lim load the last
-          // visible key's byte (key 0 when none is), which stays inside the
-          // row, and the key < lim test hides them.
+          // The row's 32 mask bytes of the tile, keys 32 kt + 8 q + 4 hi + j,
+          // as one batch of loads (one wait, no branch per key): eight aligned
+          // words (word q of half kt at byte 32 kt + 8 q + 4 hi) when the
+          // rows are 4-byte aligned and the tile lies inside the row, else
+          // 32 bytes, keys at or past lim loading the last visible key's byte
+          // (key 0 when none is) so that every read stays inside the row.
+          // The key < lim test hides what lies past lim.
           const uint8_t* mt = mrow[rg] + key0;
-          const int last = lim > 0 ? lim - 1 : 0;
-          uint8_t mb[32];
+          uint32_t mw[8];
+          if (a.mask_words && key0 + kKeys <= a.n) {
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
+            for (int q = 0; q < 8; ++q) mw[q] = reinterpret_cast<const uint32_t*>(mt)[2 * q + hi];
+          } else {
+            const int last = lim > 0 ? lim - 1 : 0;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) mb[16 * kt + v] = mt[min(32 * kt + acc_key(v, hi), last)];
+            for (int q = 0; q < 8; ++q) {
+              mw[q] = 0;
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                mw[q] |= static_cast<uint32_t>(mt[min(32 * (q >> 2) + 8 * (q & 3) + 4 * hi + j, last)]) << (8 * j);
+            }
+          }
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               const int key = 32 * kt + acc_key(v, hi);
-              vis |= (key < lim && mb[16 * kt + v] != 0) ? (1u << (16 * kt + v)) : 0u;
+              const uint32_t byte = (mw[4 * kt + (v >> 2)] >> (8 * (v & 3))) & 0xffu;
+              vis |= (key < lim && byte != 0) ? (1u << (16 * kt + v)) : 0u;
             }
         } else {
 #pragma unroll
@@ -912,6 +925,7 @@ int prefill_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.sv_b = v_strides[0]; a.sv_h = v_strides[1]; a.sv_t = v_strides[2];
   a.sm_b = mask_dev ? mask_strides[0] : 0;
   a.sm_q = mask_dev ? mask_strides[1] : 0;
+  a.mask_words = mask_dev && reinterpret_cast<uintptr_t>(mask_dev) % 4 == 0 && a.sm_b % 4 == 0 && a.sm_q % 4 == 0;
   a.so_b = out_strides[0]; a.so_t = out_strides[1]; a.so_h = out_strides[2];
   a.q_len = q_len;
   a.n = n_tokens;
