@@ -85,6 +85,20 @@ def test_random_masks_and_batches(gpu, batch_mask):
     check(q, k, v, mask=m.to(gpu), label=f"random mask batch {batch_mask}")
 
 
+@pytest.mark.parametrize("offset,pitch", [(1, 264), (3, 267), (0, 261), (4, 264)])
+def test_mask_views(gpu, offset, pitch):
+    """Boolean masks that are views: a base 1 or 3 bytes into the allocation, or an odd row
+    stride, leave the mask rows unaligned (bytes are read one by one); 4-aligned ones are
+    read as words. Both against the float64 oracle."""
+    L, n = 40, 257
+    q, k, v = workloads.prefill_inputs(60 + offset, q_len=L, n=n, device=gpu)
+    g = torch.Generator().manual_seed(pitch)
+    big = (torch.rand((1, 1, L, pitch), generator=g) < 0.5).to(gpu)
+    m = big[..., offset:offset + n]
+    assert m.stride(-2) == pitch and not m.is_contiguous()
+    check(q, k, v, mask=m, label=f"mask view offset {offset} pitch {pitch}")
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 7, 16])
 def test_key_splits(gpu, splits):
     """Splitting the keys across work-groups (LSE-merged) gives the same attention,
