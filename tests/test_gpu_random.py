@@ -1,0 +1,133 @@
+"""Seeded random sweeps of the HIP paths against the oracle: shapes, lengths,
+group sizes, element types, split lengths and masks drawn per case, so the
+parity tests reach combinations the hand-picked cases do not.
+
+- Decode (tc_decode_attention through decode_attention_batched): batches with
+  and without per-sequence lengths (empty sequences included), g in 1..8,
+  fixed or tuned split lengths, against the float64 closed form
+  (threadcut/flash_decode.py:57-69): max-abs 2e-3 fp16, 4e-3 bf16.
+- Splice (tc_splice_rope through kv.splice): random (a, c0, c) on random
+  capacities, overlapping and disjoint, against the oracle's restatement of
+  threadcut/kv.py:83-92: bit-exact.
+- Prefill (tc_prefill_attention): random chunk shapes with no mask, is_causal,
+  a causal chunk mask or a random mask, and forced key splits, against the
+  float64 closed form of attention.py:43-46: 2e-3 fp16, 1.6e-2 bf16.
+"""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+from oracle import prefill as opf
+from oracle import splice as osp
+from threadcut_amd import flash_decode, kv, prefill, workloads
+from threadcut_amd.match import Split
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+DECODE_TOL = {torch.float16: 2e-3, torch.bfloat16: 4e-3}
+PREFILL_TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+
+
+def decode_case(seed):
+    r = random.Random(seed)
+    b = r.choice([1, 1, 2, 3, 5])
+    hkv = r.choice([1, 2, 4, 8])
+    g = r.choice([1, 2, 3, 4, 5, 8])
+    n = r.choice([1, 17, 300, 1536, 4097, r.randint(1, 16000)])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    split = r.choice([None, None, 64 * r.randint(1, 64)])
+    ragged = b > 1 and r.random() < 0.6
+    lens = torch.tensor([r.choice([0, 1, n, r.randint(0, n)]) for _ in range(b)], dtype=torch.int32) \
+        if ragged else None
+    return b, hkv, g, n, dtype, split, lens
+
+
+@pytest.mark.parametrize("seed", range(120))
+def test_random_decode(gpu, seed):
+    b, hkv, g, n, dtype, split, lens = decode_case(seed)
+    print(f"case: decode seed={seed} B={b} Hkv={hkv} g={g} n={n} {dtype} split={split} "
+          f"lens={None if lens is None else lens.tolist()}", flush=True)
+    gen = torch.Generator().manual_seed(1000 + seed)
+    q = torch.randn(b, hkv, g, D, generator=gen).to(dtype)
+    k = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    v = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    scale = D ** -0.5
+    out = flash_decode.decode_attention_batched(q.to(gpu), k.to(gpu), v.to(gpu), scale,
+                                                lens=None if lens is None else lens.to(gpu), split=split)
+    torch.cuda.synchronize()
+    qn, kn, vn = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    want = od.attention_f64(qn, kn, vn, scale) if lens is None else od.decode_ragged(qn, kn, vn, lens.numpy(), scale)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= DECODE_TOL[dtype]
+
+
+class _Cache:
+    def __init__(self, layers):
+        self.layers = layers
+
+
+@pytest.mark.parametrize("seed", range(80))
+def test_random_splice(gpu, seed):
+    r = random.Random(seed)
+    layers, batch, heads = r.randint(1, 3), r.choice([1, 1, 2]), r.choice([1, 2, 8])
+    n = r.randint(2, 6000)
+    a = r.randint(0, n - 1)
+    c0 = r.choice([a, a + 1, a + r.randint(1, 47), a + r.randint(48, 700), r.randint(a, n)])
+    c0 = min(c0, n)
+    c = r.randint(0, n - c0)
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    s = Split(a, c0, c)
+    print(f"case: splice seed={seed} L={layers} B={batch} H={heads} n={n} {s} {dtype}", flush=True)
+    ks, vs = workloads.layer_caches(2000 + seed, layers, n, kv_heads=heads, batch=batch, dtype=dtype)
+    inv = workloads.inv_freq(1e6)
+    cache_layers = []
+    for k, v in zip(ks, vs):
+        layer = kv.GrowingLayer()
+        layer.update(k.to(gpu), v.to(gpu))
+        cache_layers.append(layer)
+    kv.splice(_Cache(cache_layers), s, inv)
+    torch.cuda.synchronize()
+    name = "float16" if dtype == torch.float16 else "bfloat16"
+    cos, sin = osp.rope_table(-s.gap, inv)
+    for i, layer in enumerate(cache_layers):
+        kn = ks[i].view(torch.int16).numpy().view(np.uint16) if name == "bfloat16" else ks[i].numpy()
+        vn = vs[i].view(torch.int16).numpy().view(np.uint16) if name == "bfloat16" else vs[i].numpy()
+        kb, vb, nn = osp.splice_growing(kn, vn, n, s.a, s.c0, s.c, cos, sin, name)
+        assert layer.n == nn == s.a + s.c
+        got_k = layer.kbuf[..., :n, :].cpu().view(torch.int16).numpy()
+        got_v = layer.vbuf[..., :n, :].cpu().view(torch.int16).numpy()
+        assert np.array_equal(got_k, np.asarray(kb).view(np.int16)), f"K layer {i}"
+        assert np.array_equal(got_v, np.asarray(vb).view(np.int16)), f"V layer {i}"
+
+
+@pytest.mark.parametrize("seed", range(50))
+def test_random_prefill(gpu, seed):
+    r = random.Random(seed)
+    b = r.choice([1, 1, 2])
+    hkv = r.choice([1, 2, 4, 8])
+    g = r.choice([1, 2, 4, 8])
+    mode = r.choice(["none", "causal", "chunk", "random"])
+    q_len = r.randint(1, 400)
+    n = q_len if mode == "causal" else q_len + r.randint(0, 1600)
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    splits = r.choice([None, None, r.randint(1, 8)])
+    print(f"case: prefill seed={seed} B={b} Hkv={hkv} g={g} q={q_len} n={n} {mode} {dtype} splits={splits}",
+          flush=True)
+    q, k, v = workloads.prefill_inputs(3000 + seed, batch=b, q_len=q_len, n=n, q_heads=hkv * g, kv_heads=hkv,
+                                       dtype=dtype)
+    mask = None
+    if mode == "chunk":
+        mask = workloads.causal_mask(q_len, n)
+    elif mode == "random":
+        gen = torch.Generator().manual_seed(4000 + seed)
+        mask = torch.rand((r.choice([1, b]), 1, q_len, n), generator=gen) < r.choice([0.05, 0.5, 0.95])
+    scale = D ** -0.5
+    out = prefill.prefill_attention(q.to(gpu), k.to(gpu), v.to(gpu), None if mask is None else mask.to(gpu),
+                                    scale, mode == "causal", splits=splits)
+    torch.cuda.synchronize()
+    want = opf.prefill_f64(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale,
+                           mask=None if mask is None else mask.numpy(), causal=mode == "causal")
+    assert np.abs(out.float().cpu().numpy() - want).max() <= PREFILL_TOL[dtype]
