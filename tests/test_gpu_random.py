@@ -12,6 +12,9 @@ parity tests reach combinations the hand-picked cases do not.
 - Prefill (tc_prefill_attention): random chunk shapes with no mask, is_causal,
   a causal chunk mask or a random mask, and forced key splits, against the
   float64 closed form of attention.py:43-46: 2e-3 fp16, 1.6e-2 bf16.
+- The paged cache: random page sizes, appends and prunes; pages bit-exact
+  against the contiguous splice of the same sequence, decode and prefill
+  through the pools against the float64 closed form.
 """
 import random
 
@@ -131,3 +134,66 @@ def test_random_prefill(gpu, seed):
     want = opf.prefill_f64(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale,
                            mask=None if mask is None else mask.numpy(), causal=mode == "causal")
     assert np.abs(out.float().cpu().numpy() - want).max() <= PREFILL_TOL[dtype]
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_paged(gpu, seed):
+    """The paged cache: random page size, appends in random chunks from a shuffled free
+    list, zero to two random prunes; the pages against the contiguous splice of the same
+    sequence (bit-exact), then decode and prefill against the float64 closed form on the
+    gathered keys."""
+    from threadcut_amd.paged import PagedKV
+
+    r = random.Random(seed)
+    P = r.choice([16, 32, 48, 64, 128])
+    hkv, g = r.choice([(8, 4), (4, 8), (2, 2), (8, 1)])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    n = r.randint(1, 5000)
+    name = "float16" if dtype == torch.float16 else "bfloat16"
+    pages = -(-n // P) * 2 + 8
+    cache = PagedKV(1, hkv, pages, P, dtype=dtype, device=gpu)
+    r.shuffle(cache.table.free)
+    gen = torch.Generator().manual_seed(5000 + seed)
+    k = torch.randn(hkv, n, D, generator=gen).to(dtype)
+    v = torch.randn(hkv, n, D, generator=gen).to(dtype)
+    done = 0
+    while done < n:
+        m = min(n - done, r.choice([1, 7, 16, 64, 300, 1500]))
+        cache.append(0, [k[:, done:done + m].to(gpu)], [v[:, done:done + m].to(gpu)])
+        done += m
+    inv = workloads.inv_freq(1e6)
+    kn = (k.view(torch.int16).numpy().view(np.uint16) if name == "bfloat16" else k.numpy())[None]
+    vn = (v.view(torch.int16).numpy().view(np.uint16) if name == "bfloat16" else v.numpy())[None]
+    splits = []
+    for _ in range(r.choice([0, 1, 2])):
+        cur = cache.length()
+        if cur < 2:
+            break
+        a = r.randint(0, cur - 1)
+        c0 = r.randint(a, cur)
+        c = r.randint(0, cur - c0)
+        s = Split(a, c0, c)
+        splits.append(s)
+        cache.prune(0, s, inv)
+        cos, sin = osp.rope_table(-s.gap, inv)
+        kn, vn, nn = osp.splice_growing(kn, vn, cur, s.a, s.c0, s.c, cos, sin, name)
+        kn, vn = kn[..., :nn, :], vn[..., :nn, :]
+    print(f"case: paged seed={seed} P={P} Hkv={hkv} g={g} n={n} {dtype} prunes={splits}", flush=True)
+    gk, gv = cache.gather(0)
+    torch.cuda.synchronize()
+    assert gk.shape[1] == kn.shape[-2] == cache.length()
+    assert np.array_equal(gk.cpu().view(torch.int16).numpy(), np.asarray(kn[0]).view(np.int16))
+    assert np.array_equal(gv.cpu().view(torch.int16).numpy(), np.asarray(vn[0]).view(np.int16))
+    keys, vals = gk.cpu().float().numpy()[None], gv.cpu().float().numpy()[None]
+    q = torch.randn(1, hkv, g, D, generator=gen).to(dtype)
+    out = cache.decode(0, q.to(gpu), D ** -0.5)
+    torch.cuda.synchronize()
+    want = od.attention_f64(q.float().numpy(), keys, vals, D ** -0.5)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= DECODE_TOL[dtype]
+    nq = r.randint(1, min(cache.length(), 200)) if cache.length() else 0
+    if nq:
+        qp = torch.randn(1, nq, hkv * g, D, generator=gen).to(dtype).transpose(1, 2)
+        outp = cache.prefill(0, qp.to(gpu), D ** -0.5, causal=False)
+        torch.cuda.synchronize()
+        wantp = opf.prefill_f64(qp.float().numpy(), keys, vals, D ** -0.5)
+        assert np.abs(outp.float().cpu().numpy() - wantp).max() <= PREFILL_TOL[dtype]
