@@ -66,12 +66,19 @@ def read_traffic(name):
     return None
 
 
-def time_graph(graph, steps, warmup):
+def time_graph(graph, steps, warmup, min_warm_ms=0.0):
+    """ms per replay over `steps` replays after `warmup` untimed ones; with min_warm_ms,
+    untimed replays continue until that much time has passed (the clocks of this part
+    take milliseconds to ramp up after the device idled, e.g. during input generation)."""
     import torch
 
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
+        graph.replay()
+        torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -286,7 +293,7 @@ def stream_read_lib():
     return lib
 
 
-def measure_sweep(dev, n, steps, warmup, split, only):
+def measure_sweep(dev, n, steps, warmup, split, only, min_warm_ms=0.0):
     """36 sequential decode calls at n tokens (own K/V per layer) as one HIP graph; the
     partial pass alone and the streaming-read yardstick as graphs over the same layers."""
     import torch
@@ -309,9 +316,9 @@ def measure_sweep(dev, n, steps, warmup, split, only):
 
     result = {"splits": S, "split_tokens": plans[0].split_tokens}
     if only in (None, "decode"):
-        result["ms"] = time_graph(capture(step), steps, warmup)
+        result["ms"] = time_graph(capture(step), steps, warmup, min_warm_ms)
     if only in (None, "partial"):
-        result["ms_partial"] = time_graph(capture(step_partial), steps, warmup)
+        result["ms_partial"] = time_graph(capture(step_partial), steps, warmup, min_warm_ms)
     if only in (None, "yardstick"):
         ylib = stream_read_lib()
         sink = torch.zeros(S * HKV, dtype=torch.int32, device=dev)
@@ -323,7 +330,7 @@ def measure_sweep(dev, n, steps, warmup, split, only):
                 if ylib.tc_bench_stream_read(k.data_ptr(), v.data_ptr(), kst, vst, n, HKV, S, sink.data_ptr(), s_):
                     raise RuntimeError("tc_bench_stream_read failed")
 
-        result["ms_yardstick"] = time_graph(capture(step_read), steps, warmup)
+        result["ms_yardstick"] = time_graph(capture(step_read), steps, warmup, min_warm_ms)
     del plans, ks, vs
     torch.cuda.empty_cache()
     return result
@@ -333,7 +340,7 @@ def _time_plan(plan, steps, reps=10):
     def step():
         for _ in range(reps):
             plan.run()
-    ms = time_graph(capture(step), steps, 3)
+    ms = time_graph(capture(step), steps, 3, min_warm_ms=50.0)
     return ms * 1e3 / reps
 
 
@@ -948,7 +955,7 @@ def main():
     if not args.no_reports:
         sweep = {}
         for m in SWEEP:
-            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None)
+            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None, 50.0)
             sweep[str(m)] = summarize(r, decode_bytes(m))
         line["sweep_36_layers"] = sweep
         line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
