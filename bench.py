@@ -383,10 +383,34 @@ def measure_long(dev, batch, steps):
     plan = flash_decode.DecodePlan(q, k, v, D ** -0.5, out)
     us = _time_plan(plan, steps)
     nbytes = decode_bytes(n, batch)
+    r = {"us_per_call": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes,
+         "splits": plan.splits, "split_tokens": plan.split_tokens}
+    if batch == 1:
+        # The partial pass alone and its loads alone (the streaming-read yardstick).
+        from threadcut_amd import _lib
+
+        reps = 10
+        ylib = stream_read_lib()
+        sink = torch.zeros(plan.splits * HKV, dtype=torch.int32, device=dev)
+        kst, vst = _lib.i64x2(k.stride(1), k.stride(2)), _lib.i64x2(v.stride(1), v.stride(2))
+
+        def partial():
+            for _ in range(reps):
+                plan.run_partial()
+
+        def loads():
+            for _ in range(reps):
+                if ylib.tc_bench_stream_read(k.data_ptr(), v.data_ptr(), kst, vst, n, HKV, plan.splits,
+                                             sink.data_ptr(), _lib.stream_of(dev)):
+                    raise RuntimeError("tc_bench_stream_read failed")
+
+        pus = time_graph(capture(partial), steps, 3, min_warm_ms=50.0) * 1e3 / reps
+        yus = time_graph(capture(loads), steps, 3, min_warm_ms=50.0) * 1e3 / reps
+        r.update({"partial_us": round(pus, 2), "yardstick_us": round(yus, 2),
+                  "partial_over_yardstick": round(pus / yus, 4)})
     del k, v
     torch.cuda.empty_cache()
-    return {"us_per_call": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes,
-            "splits": plan.splits, "split_tokens": plan.split_tokens}
+    return r
 
 
 def measure_append(dev, n, steps):
