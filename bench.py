@@ -340,7 +340,7 @@ def _time_plan(plan, steps, reps=10):
     def step():
         for _ in range(reps):
             plan.run()
-    ms = time_graph(capture(step), steps, 3, min_warm_ms=50.0)
+    ms = time_graph(capture(step), steps, 3, min_warm_ms=250.0)
     return ms * 1e3 / reps
 
 
@@ -404,8 +404,8 @@ def measure_long(dev, batch, steps):
                                              sink.data_ptr(), _lib.stream_of(dev)):
                     raise RuntimeError("tc_bench_stream_read failed")
 
-        pus = time_graph(capture(partial), steps, 3, min_warm_ms=50.0) * 1e3 / reps
-        yus = time_graph(capture(loads), steps, 3, min_warm_ms=50.0) * 1e3 / reps
+        pus = time_graph(capture(partial), steps, 3, min_warm_ms=250.0) * 1e3 / reps
+        yus = time_graph(capture(loads), steps, 3, min_warm_ms=250.0) * 1e3 / reps
         r.update({"partial_us": round(pus, 2), "yardstick_us": round(yus, 2),
                   "partial_over_yardstick": round(pus / yus, 4)})
     del k, v
@@ -979,7 +979,7 @@ def main():
     if not args.no_reports:
         sweep = {}
         for m in SWEEP:
-            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None, 50.0)
+            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None, 250.0)
             sweep[str(m)] = summarize(r, decode_bytes(m))
         line["sweep_36_layers"] = sweep
         line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
