@@ -88,6 +88,20 @@ def time_graph(graph, steps, warmup, min_warm_ms=0.0):
     return start.elapsed_time(stop) / steps  # ms per replay
 
 
+WARM_MS = 250.0  # untimed work before each report that times eager calls or its own inputs
+
+
+def warm_eager(fn, ms=WARM_MS):
+    """Calls fn (enqueued work) until `ms` of wall time has passed, synchronizing each
+    time: the device then runs at its steady speed when the timed calls start."""
+    import torch
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        fn()
+        torch.cuda.synchronize()
+
+
 def capture(fn):
     import torch
 
@@ -240,6 +254,7 @@ def bench_splice(dev, steps, warmup):
         for _ in range(warm):
             run()
         torch.cuda.synchronize()
+        warm_eager(run)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
@@ -340,7 +355,7 @@ def _time_plan(plan, steps, reps=10):
     def step():
         for _ in range(reps):
             plan.run()
-    ms = time_graph(capture(step), steps, 3, min_warm_ms=250.0)
+    ms = time_graph(capture(step), steps, 3, min_warm_ms=WARM_MS)
     return ms * 1e3 / reps
 
 
@@ -404,8 +419,8 @@ def measure_long(dev, batch, steps):
                                              sink.data_ptr(), _lib.stream_of(dev)):
                     raise RuntimeError("tc_bench_stream_read failed")
 
-        pus = time_graph(capture(partial), steps, 3, min_warm_ms=250.0) * 1e3 / reps
-        yus = time_graph(capture(loads), steps, 3, min_warm_ms=250.0) * 1e3 / reps
+        pus = time_graph(capture(partial), steps, 3, min_warm_ms=WARM_MS) * 1e3 / reps
+        yus = time_graph(capture(loads), steps, 3, min_warm_ms=WARM_MS) * 1e3 / reps
         r.update({"partial_us": round(pus, 2), "yardstick_us": round(yus, 2),
                   "partial_over_yardstick": round(pus / yus, 4)})
     del k, v
@@ -485,6 +500,7 @@ def measure_mfma_ceiling(dev, iters=2000):
                 raise RuntimeError("tc_bench_mfma_ceiling failed")
         run()
         torch.cuda.synchronize()
+        warm_eager(run)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(3):
@@ -513,6 +529,7 @@ def measure_prefill(dev, steps, only_case=None):
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
+        warm_eager(fn)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(iters):
@@ -828,6 +845,7 @@ def measure_paged_prefill(dev, page_tokens, iters=10):
     def timed(fn):
         fn()
         torch.cuda.synchronize()
+        warm_eager(fn)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(iters):
@@ -979,7 +997,7 @@ def main():
     if not args.no_reports:
         sweep = {}
         for m in SWEEP:
-            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None, 250.0)
+            r = result if m == n else measure_sweep(dev, m, max(20, args.steps // 4), 5, args.split, None, WARM_MS)
             sweep[str(m)] = summarize(r, decode_bytes(m))
         line["sweep_36_layers"] = sweep
         line["ragged_16"] = measure_ragged(dev, max(10, args.steps // 10))
