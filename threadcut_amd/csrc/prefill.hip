@@ -302,6 +302,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     const int64_t key = tile * kKeys + lane;
     return key < a.n ? toff[key] : kNoRow;
   };
+  // Load c of the eight of a stage (c < 4: K chunk t + 256 c; else V row c - 4), the
+  // chunks of load_stage / load_stage_paged.
+  auto stage_part = [&](Stage& st_, int64_t tile, int32_t idx, int c) {
+    const int tt = threadIdx.x;
+    const int i = c & 3;
+    if constexpr (PAGED) {
+      const int ln = tt & 63;
+      const int key = c < 4 ? (ln >> 4) + 4 * (tt >> 6) + 16 * i : 4 * ((ln >> 4) + 4 * (tt >> 6)) + i;
+      const int32_t off = __builtin_amdgcn_ds_bpermute(4 * key, idx) + 16 * (tt & 15);
+      if (c < 4)
+        st_.k[i] = bload(prk, off);
+      else
+        st_.v[i] = bload(prv, off);
+    } else {
+      const int64_t key0 = tile * kKeys;
+      const int64_t rows = a.n - key0 < kKeys ? a.n - key0 : kKeys;
+      if (c < 4) {
+        const int cc = tt + 256 * i;
+        st_.k[i] = bload(rsrc(kslab + key0 * row_k, rows * row_k), static_cast<int32_t>((cc >> 4) * row_k + 16 * (cc & 15)));
+      } else {
+        st_.v[i] = bload(rsrc(vslab + key0 * row_v, rows * row_v),
+                         static_cast<int32_t>((4 * (tt >> 4) + i) * row_v + 16 * (tt & 15)));
+      }
+    }
+  };
   auto stage = [&](Stage& st_, int64_t tile, int32_t idx) {
     if constexpr (PAGED)
       load_stage_paged(st_, prk, prv, idx);
@@ -391,7 +416,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   int buf = 0;
   while (t < nt) {
     const bool more = tn < nt;
-    if (more) stage(st, tn, rows_n);
+    const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, staged during this QK^T
     const int64_t tnn = more ? next_active(tn + 1) : nt;
     const int cls_nn = tnn < nt ? tile_class(tnn) : TILE_SKIP;
     if constexpr (PAGED) rows_n = tnn < nt ? tile_rows(tnn) : kNoRow;
@@ -403,7 +428,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     // feeds kGroups MFMAs; the two 32-key halves are independent chains.
     // The K fragments are read four chunks ahead of their MFMAs; the
     // scheduling barriers keep the compiler from pulling the reads back next
-    // to their use (it otherwise waits out each read's latency).
+    // to their use (it otherwise waits out each read's latency). The next
+    // tile's eight global loads per thread go out one per chunk, between the
+    // MFMAs, instead of as one burst before them.
     float16v s[kGroups][2];
 #pragma unroll
     for (int rg = 0; rg < kGroups; ++rg)
@@ -422,6 +449,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int c = 0; c < 8; ++c) {
         const uint4 k0 = kf[c & 3][0], k1 = kf[c & 3][1];
         if (c + 4 < 8) { kf[c & 3][0] = kfrag(c + 4, 0); kf[c & 3][1] = kfrag(c + 4, 1); }
+        if (more) stage_part(st, tn, rows_tn, c);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int rg = 0; rg < kGroups; ++rg) {
