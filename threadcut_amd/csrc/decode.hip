@@ -92,7 +92,7 @@ struct PartialArgs {
   int64_t skn_b, skn_h, svn_b, svn_h;
   uint16_t* k_w;
   uint16_t* v_w;
-  // Paged cache (decode_partial_kernel<DT, true>): k and v are page pools
+  // Paged cache (decode_partial_kernel<DT, true, *>): k and v are page pools
   // [pages, H, P, D] with element strides (sk_b, sk_h, sk_t) = (page, head,
   // token). Sequence b's keys are the tiles tile_tab[b * max_tiles + i],
   // i < tiles[b], each {page, first slot, rows, 0}: rows (<= 16) consecutive
@@ -245,7 +245,9 @@ __host__ __device__ constexpr int vt_word(int d) { return 8 * d + 4 * (d >> 3); 
 constexpr int kVtWords = vt_word(kHeadDim);   // per wave
 constexpr float kLazyMax = 8.f;               // log2 units the running maximum may lag
 
-template <int DT, bool PAGED>
+// APPEND: the kernel attends (and writes) the new token of an append call
+// (a.k_new != null); the other instantiation carries none of that code.
+template <int DT, bool PAGED, bool APPEND>
 __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const PartialArgs a) {
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
@@ -258,8 +260,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;   // head column (also the token row of the K operand)
   const int g = lane >> 4;   // lane group
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
+  // Grid (heads, splits, batch), the KV head fastest: consecutive work-groups
+  // go to consecutive XCDs, so with 8 KV heads every split of head h runs on
+  // XCD h and its partials stay in that XCD's L2 for the combine.
+  const int h = blockIdx.x;
+  const int split = blockIdx.y;
   const int b = blockIdx.z;
 
   // Paged: the pools' head slabs, pages added per tile; otherwise sequence b's slabs.
@@ -268,7 +273,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   const int32_t row_k = static_cast<int32_t>(a.sk_t) * 2, row_v = static_cast<int32_t>(a.sv_t) * 2;
   __asm__ volatile("" ::"s"(kslab), "s"(vslab));
   const int32_t nt = static_cast<int32_t>(a.n);
-  const int32_t len_cap = a.k_new ? nt - 1 : nt;
+  const int32_t len_cap = APPEND ? nt - 1 : nt;
   int32_t len = len_cap;
   const int32_t* tab = nullptr;
   int32_t last_tile = -1;  // paged append: the tile whose last row is the new token's slot
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     tab = a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4;
     if (a.tok_off)
       plen = min(max(a.lens[b], 0), static_cast<int32_t>(a.tok_pitch) - 1);
-    else if (a.k_new)
+    else if (APPEND)
       last_tile = ntiles - 1;
   } else if (a.lens) {
     len = min(max(a.lens[b], 0), len_cap);
@@ -388,7 +393,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     // Lazy running maximum: moves only when the tile's exceeds it by kLazyMax.
     const float mn = (tmax > m + kLazyMax || m == neg_inf()) ? tmax : m;
     const float ms = (mn == neg_inf()) ? 0.f : mn;
-    if (__any(mn != m)) {
+    // Rescale what was accumulated (nothing while m is still -inf: acc and l are zero).
+    if (__any(mn != m && m != neg_inf())) {
       const float alpha = __builtin_amdgcn_exp2f(m - ms);  // 0 while nothing was seen
 #pragma unroll
       for (int bm = 0; bm < 8; ++bm) acc[bm] *= alpha;
@@ -427,7 +433,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     }
   }
 
-  if (a.k_new && split == 0 && wave == 0) {
+  if (APPEND && split == 0 && wave == 0) {
     // The appended token as a tile whose only row is token 0 (the buffer
     // range is one row, so the other rows read zero and are masked).
     const char* kn = reinterpret_cast<const char*>(a.k_new + b * a.skn_b + h * a.skn_h);
@@ -517,44 +523,17 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   }
 }
 
-// Combine: one 256-thread work-group per (32-dim quarter, query head; kv
-// head; sequence), a 3-D grid. Thread (sl, dq) folds splits sl, sl + 32, ... of dims
-// 4*dq .. 4*dq+3 with a running (max, sum, weighted o); the 32 split lanes are
-// merged with wave shuffles and one LDS exchange. All loads are issued before
-// any is consumed, so a call costs one memory round trip.
-constexpr int kCombineLanes = 32;   // split lanes per work-group
-constexpr int kCombineQuads = 8;    // float4 dim quads per work-group (32 dims)
+// Combine: one wave per (query head, kv head, sequence), a 3-D grid. Lane
+// (half, quad) takes dims 4 quad .. 4 quad + 3 of splits half, half + 2,
+// half + 4, ...: in rounds of kCombineRound splits per lane, every load of a
+// round issued before any is consumed (one memory round trip per round; one
+// round covers up to 2 * kCombineRound splits). Each round folds its splits
+// into a running (max, sum, weighted o) with one exponential per split; one
+// permlane32 swap merges the two halves.
+constexpr int kCombineRound = 16;   // splits per lane and round
 
-struct Acc4 {
-  float m, l;
-  float4 o;
-};
-
-__device__ __forceinline__ Acc4 merge(const Acc4& a, const Acc4& b) {
-  const float M = fmaxf(a.m, b.m);
-  const float Ms = (M == neg_inf()) ? 0.f : M;
-  const float fa = __builtin_amdgcn_exp2f((a.m - Ms) * kLog2e);
-  const float fb = __builtin_amdgcn_exp2f((b.m - Ms) * kLog2e);
-  Acc4 r;
-  r.m = M;
-  r.l = a.l * fa + b.l * fb;
-  r.o = make_float4(a.o.x * fa + b.o.x * fb, a.o.y * fa + b.o.y * fb, a.o.z * fa + b.o.z * fb,
-                    a.o.w * fa + b.o.w * fb);
-  return r;
-}
-
-// Merges of a lane's state with its partner's, without LDS: lane ^ 8 by DPP
-// row_ror:8; lanes ^ 16 and ^ 32 by v_permlane16/32_swap, whose two results
-// hold the pair's two states in every lane (merge is symmetric).
-__device__ __forceinline__ Acc4 merge_xor8(const Acc4& a) {
-  Acc4 p;
-  p.m = dpp<DPP_ROW_ROR8>(a.m);
-  p.l = dpp<DPP_ROW_ROR8>(a.l);
-  p.o = make_float4(dpp<DPP_ROW_ROR8>(a.o.x), dpp<DPP_ROW_ROR8>(a.o.y), dpp<DPP_ROW_ROR8>(a.o.z),
-                    dpp<DPP_ROW_ROR8>(a.o.w));
-  return merge(a, p);
-}
-
+// x of the lane pair (l, l ^ 16) or (l, l ^ 32): the lower row's value in lo,
+// the upper row's in hi, in both lanes.
 template <bool ROW32>
 __device__ __forceinline__ void swap_pair(float x, float& lo, float& hi) {
   const uint32_t u = __float_as_uint(x);
@@ -564,70 +543,84 @@ __device__ __forceinline__ void swap_pair(float x, float& lo, float& hi) {
   hi = __uint_as_float(r[1]);
 }
 
-template <bool ROW32>
-__device__ __forceinline__ Acc4 merge_swap(const Acc4& a) {
-  Acc4 x, y;
-  swap_pair<ROW32>(a.m, x.m, y.m);
-  swap_pair<ROW32>(a.l, x.l, y.l);
-  swap_pair<ROW32>(a.o.x, x.o.x, y.o.x);
-  swap_pair<ROW32>(a.o.y, x.o.y, y.o.y);
-  swap_pair<ROW32>(a.o.z, x.o.z, y.o.z);
-  swap_pair<ROW32>(a.o.w, x.o.w, y.o.w);
-  return merge(x, y);
-}
-
 template <int DT>
-__global__ __launch_bounds__(256) void decode_combine_kernel(const CombineArgs a) {
+__global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a) {
   using E = Elem<DT>;
-  __shared__ Acc4 s_part[4][kCombineQuads];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int dq = tid & (kCombineQuads - 1);
-  const int sl = tid / kCombineQuads;
+  const int lane = threadIdx.x;
+  const int quad = lane & 31;
+  const int half = lane >> 5;
+  // Grid (heads, batch, group), the KV head fastest: with 8 heads, head h's
+  // work-groups run on XCD h, where the partial kernel wrote its partials.
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int g = blockIdx.z;
   const int G = a.group;
   const int S = a.splits;
-  // Grid (4 * G, heads, batch): no index division before the loads.
-  const int quarter = blockIdx.x & 3;
-  const int g = blockIdx.x >> 2;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
   const int64_t bh = static_cast<int64_t>(b) * a.heads + h;
-  const int dim0 = 32 * quarter + 4 * dq;
+  // Buffer ranges over this (sequence, head)'s partials: loads past them read zero.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.o_part + bh * S * G * kHeadDim, S * G * kHeadDim * 4);
+  const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse_part + bh * S * G, S * G * 4);
+  // Per-lane byte offsets (split `half` of a round); the round's split r0 + 2 j
+  // adds a wave-uniform offset.
+  const int32_t o_split = G * kHeadDim * 4;  // bytes between splits
+  const int32_t o_lane = half * o_split + (g * kHeadDim + 4 * quad) * 4;
+  const int32_t l_lane = (half * G + g) * 4;
 
-  const float* lse = a.lse_part + bh * S * G + g;
-  const float* o = a.o_part + (bh * S * G + g) * kHeadDim + dim0;
-
-  Acc4 acc;
-  acc.m = neg_inf();
-  acc.l = 0.f;
-  acc.o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int s = sl; s < S; s += kCombineLanes) {
-    const float ls = lse[static_cast<int64_t>(s) * G];
-    const float4 ov = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(s) * G * kHeadDim);
-    Acc4 one;
-    one.m = ls;
-    one.l = 1.f;
-    one.o = ov;
-    acc = merge(acc, one);
-  }
-  // Split lanes inside the wave: lanes dq + 8 * k, k = 0..7.
-  acc = merge_xor8(acc);
-  acc = merge_swap<false>(acc);
-  acc = merge_swap<true>(acc);
-  if (lane < kCombineQuads) s_part[wave][lane] = acc;
-  __syncthreads();
-  if (tid < kCombineQuads) {
-    Acc4 r = s_part[0][tid];
+  float M = neg_inf(), L = 0.f;
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r0 = 0; r0 < S; r0 += 2 * kCombineRound) {
+    u32x4 ov[kCombineRound];
+    float ls[kCombineRound];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) r = merge(r, s_part[w][tid]);
-    const bool empty = (r.m == neg_inf());
-    const float inv = empty ? 0.f : 1.f / r.l;
-    const uint32_t w0 = E::bits(r.o.x * inv) | (E::bits(r.o.y * inv) << 16);
-    const uint32_t w1 = E::bits(r.o.z * inv) | (E::bits(r.o.w * inv) << 16);
-    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 32 * quarter + 4 * tid;
+    for (int j = 0; j < kCombineRound; ++j) {
+      const int32_t s0 = r0 + 2 * j;
+      ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, o_lane, s0 * o_split, 0);
+      ls[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, l_lane, s0 * G * 4, 0));
+    }
+    // Every load of the round is in flight before the first is consumed.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kCombineRound; ++j)
+      if (r0 + 2 * j + half >= S) ls[j] = neg_inf();  // past the last split (the load read zero)
+    float mr = ls[0];
+#pragma unroll
+    for (int j = 1; j < kCombineRound; ++j) mr = fmaxf(mr, ls[j]);
+    const float Mn = fmaxf(M, mr);
+    const float Ms = (Mn == neg_inf()) ? 0.f : Mn;
+    const float f = __builtin_amdgcn_exp2f((M - Ms) * kLog2e);  // 0 while nothing was seen
+    L *= f;
+    O.x *= f; O.y *= f; O.z *= f; O.w *= f;
+#pragma unroll
+    for (int j = 0; j < kCombineRound; ++j) {
+      const float w = __builtin_amdgcn_exp2f((ls[j] - Ms) * kLog2e);
+      L += w;
+      O.x += w * __uint_as_float(ov[j].x);
+      O.y += w * __uint_as_float(ov[j].y);
+      O.z += w * __uint_as_float(ov[j].z);
+      O.w += w * __uint_as_float(ov[j].w);
+    }
+    M = Mn;
+  }
+  // Merge the two halves (lanes l and l ^ 32).
+  float Mo, Mx;
+  swap_pair<true>(M, Mo, Mx);
+  Mx = fmaxf(Mo, Mx);
+  const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
+  const float f = __builtin_amdgcn_exp2f((M - Ms) * kLog2e);
+  float lo, hi;
+  swap_pair<true>(L * f, lo, hi);
+  const float Lt = lo + hi;
+  float4 Ot;
+  swap_pair<true>(O.x * f, lo, hi); Ot.x = lo + hi;
+  swap_pair<true>(O.y * f, lo, hi); Ot.y = lo + hi;
+  swap_pair<true>(O.z * f, lo, hi); Ot.z = lo + hi;
+  swap_pair<true>(O.w * f, lo, hi); Ot.w = lo + hi;
+  if (half == 0) {
+    // An empty cache (no splits, or every split empty) gives zeros.
+    const float inv = (Mx == neg_inf()) ? 0.f : 1.f / Lt;
+    const uint32_t w0 = E::bits(Ot.x * inv) | (E::bits(Ot.y * inv) << 16);
+    const uint32_t w1 = E::bits(Ot.z * inv) | (E::bits(Ot.w * inv) << 16);
+    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 4 * quad;
     *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
   }
 }
@@ -655,14 +648,24 @@ int check_common(int batch, int kv_heads, int group, int head_dim, int dtype) {
   return TC_OK;
 }
 
+inline dim3 partial_grid(const PartialArgs& a, int batch) { return dim3(a.heads, a.splits, batch); }
+
+template <int DT, bool PAGED>
+void launch_partial_paged(const PartialArgs& a, int batch, hipStream_t stream) {
+  if (a.k_new)
+    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, true>), partial_grid(a, batch), dim3(64 * kWaves), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, false>), partial_grid(a, batch), dim3(64 * kWaves), 0,
+                       stream, a);
+}
+
 template <int DT>
 hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream) {
   if (a.tile_tab)
-    hipLaunchKernelGGL((decode_partial_kernel<DT, true>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0, stream,
-                       a);
+    launch_partial_paged<DT, true>(a, batch, stream);
   else
-    hipLaunchKernelGGL((decode_partial_kernel<DT, false>), dim3(a.splits, a.heads, batch), dim3(64 * kWaves), 0,
-                       stream, a);
+    launch_partial_paged<DT, false>(a, batch, stream);
   return hipGetLastError();
 }
 
@@ -882,12 +885,12 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   a.heads = kv_heads;
   a.group = group;
   a.splits = num_splits;
-  const dim3 grid(4 * group, kv_heads, batch);
+  const dim3 grid(kv_heads, batch, group), block(64);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == TC_DTYPE_F16)
-    hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_F16>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_F16>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_BF16>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_BF16>), grid, block, 0, s, a);
   return hip_status(hipGetLastError(), "decode_combine launch");
 }
 
