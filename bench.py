@@ -301,6 +301,8 @@ def stream_read_lib():
     lib = ctypes.CDLL(build.BENCH_LIB)
     lib.tc_bench_mfma_ceiling.restype = ctypes.c_int
     lib.tc_bench_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.tc_bench_empty_launch.restype = ctypes.c_int
+    lib.tc_bench_empty_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.tc_bench_stream_read.restype = ctypes.c_int
     lib.tc_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
                                          ctypes.POINTER(ctypes.c_int64), ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -346,6 +348,14 @@ def measure_sweep(dev, n, steps, warmup, split, only, min_warm_ms=0.0):
                     raise RuntimeError("tc_bench_stream_read failed")
 
         result["ms_yardstick"] = time_graph(capture(step_read), steps, warmup, min_warm_ms)
+
+        def step_empty():
+            s_ = _lib.stream_of(dev)
+            for _ in range(LAYERS):
+                if ylib.tc_bench_empty_launch(S * HKV, sink.data_ptr(), s_):
+                    raise RuntimeError("tc_bench_empty_launch failed")
+
+        result["ms_empty"] = time_graph(capture(step_empty), steps, warmup, min_warm_ms)
     del plans, ks, vs
     torch.cuda.empty_cache()
     return result
@@ -992,7 +1002,10 @@ def main():
                       "us_per_launch": round(yard_us, 3),
                       "GB/s": round(per_call_bytes / (yard_us * 1e-6) / 1e9, 1),
                       "frac": round(per_call_bytes / (yard_us * 1e-6) / 1e9 / PEAK_GBS, 4),
-                      "partial_over_yardstick": round(partial_us / yard_us, 4)},
+                      "partial_over_yardstick": round(partial_us / yard_us, 4),
+                      "empty_launch_us": round(result["ms_empty"] * 1e3 / LAYERS, 3),
+                      "empty_launch_what": "an empty kernel of the partial's grid size, 36 dependent launches in "
+                                           "one graph: what one launch costs in the chain before any work"},
     }
     if not args.no_reports:
         sweep = {}

@@ -1,6 +1,6 @@
 // Streaming-read yardstick for the decode partial kernel (measurement only;
 // not part of the decode ABI). It issues exactly the partial kernel's loads
-// and nothing else: grid (S splits, Hkv heads), 256 threads, each wave
+// and nothing else: grid (Hkv heads, S splits), 256 threads, each wave
 // taking 16-token tiles s*4 + w, + 4S, ... of its head (the round-robin
 // schedule of tc_decode_attention), per lane and tile four 16-byte K loads
 // (token lane % 16, bytes 64 i + 16 (lane / 16)) and four 16-byte V loads
@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const Args a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nl = lane & 15, g = lane >> 4;
-  const int s = blockIdx.x, h = blockIdx.y;
+  const int h = blockIdx.x, s = blockIdx.y;
   const int row_k = static_cast<int>(a.sk_t) * 2, row_v = static_cast<int>(a.sv_t) * 2;
   const char* kslab = reinterpret_cast<const char*>(a.k + h * a.sk_h);
   const char* vslab = reinterpret_cast<const char*>(a.v + h * a.sv_h);
@@ -70,6 +70,12 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const Args a) {
   if (acc == 0x9e3779b9u) a.sink[blockIdx.y * gridDim.x + blockIdx.x] = acc;
 }
 
+// A kernel that does nothing: a graph of these measures what one launch costs
+// in a chain of dependent launches.
+__global__ __launch_bounds__(256) void empty_kernel(uint32_t* sink, int never) {
+  if (never == 0x7fffffff && threadIdx.x == 0) sink[blockIdx.x] = 1u;
+}
+
 }  // namespace
 
 extern "C" {
@@ -87,7 +93,16 @@ int tc_bench_stream_read(const void* k, const void* v, const int64_t k_strides[2
     return 1;
   Args a{static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), k_strides[0], k_strides[1],
          v_strides[0], v_strides[1], n_tokens, splits, static_cast<uint32_t*>(sink)};
-  hipLaunchKernelGGL(stream_read_kernel, dim3(splits, kv_heads), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(kv_heads, splits), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// One launch of an empty kernel of `blocks` 256-thread work-groups. `sink`
+// holds blocks words (never written). Returns 0 or 1.
+int tc_bench_empty_launch(int blocks, void* sink, void* stream) {
+  if (!sink || blocks < 1 || blocks > 65535) return 1;
+  hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint32_t*>(sink), 0);
   return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
