@@ -140,8 +140,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t by
                                            0x00020000);
 }
 
-__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, int32_t off) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, int32_t off, int32_t soff = 0) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -302,19 +302,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     const int64_t key = tile * kKeys + lane;
     return key < a.n ? toff[key] : kNoRow;
   };
+  // Paged: when a tile's 64 keys are consecutive rows of one page (key k at
+  // offset first + k * row), the offset of key 0, else -1 (also for a tile
+  // that runs past n). Wave-uniform.
+  auto contiguous_from = [&](int32_t idx) -> int32_t {
+    const int32_t first = __builtin_amdgcn_readfirstlane(idx);
+    const bool apart = static_cast<uint32_t>(idx) != static_cast<uint32_t>(first) + lane * static_cast<uint32_t>(row_k);
+    return (first >= 0 && __builtin_amdgcn_ballot_w64(apart) == 0) ? first : -1;
+  };
   // Load c of the eight of a stage (c < 4: K chunk t + 256 c; else V row c - 4), the
-  // chunks of load_stage / load_stage_paged.
-  auto stage_part = [&](Stage& st_, int64_t tile, int32_t idx, int c) {
+  // chunks of load_stage / load_stage_paged. Paged: a row's offset is first +
+  // key * row for a contiguous tile (first >= 0), else taken from the lane of idx
+  // that holds it.
+  auto stage_part = [&](Stage& st_, int64_t tile, int32_t idx, int32_t first, int c) {
     const int tt = threadIdx.x;
     const int i = c & 3;
     if constexpr (PAGED) {
       const int ln = tt & 63;
-      const int key = c < 4 ? (ln >> 4) + 4 * (tt >> 6) + 16 * i : 4 * ((ln >> 4) + 4 * (tt >> 6)) + i;
-      const int32_t off = __builtin_amdgcn_ds_bpermute(4 * key, idx) + 16 * (tt & 15);
-      if (c < 4)
-        st_.k[i] = bload(prk, off);
-      else
-        st_.v[i] = bload(prv, off);
+      const int kq = (ln >> 4) + 4 * (tt >> 6);  // K chunk t + 256 i: key kq + 16 i; V row i: key 4 kq + i
+      const int key = c < 4 ? kq + 16 * i : 4 * kq + i;
+      if (first >= 0) {
+        // The lane's part of the offset in a register, the tile's and the chunk's in a scalar.
+        const int32_t row = static_cast<int32_t>(row_k);
+        const int32_t lane_off = (c < 4 ? kq : 4 * kq) * row + 16 * (tt & 15);
+        const int32_t soff = first + (c < 4 ? 16 * i : i) * row;
+        if (c < 4)
+          st_.k[i] = bload(prk, lane_off, soff);
+        else
+          st_.v[i] = bload(prv, lane_off, soff);
+      } else {
+        const int32_t off = __builtin_amdgcn_ds_bpermute(4 * key, idx) + 16 * (tt & 15);
+        if (c < 4)
+          st_.k[i] = bload(prk, off);
+        else
+          st_.v[i] = bload(prv, off);
+      }
     } else {
       const int64_t key0 = tile * kKeys;
       const int64_t rows = a.n - key0 < kKeys ? a.n - key0 : kKeys;
@@ -417,6 +439,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   while (t < nt) {
     const bool more = tn < nt;
     const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, staged during this QK^T
+    int32_t first_tn = -1;
+    if constexpr (PAGED) first_tn = more ? contiguous_from(rows_tn) : -1;
     const int64_t tnn = more ? next_active(tn + 1) : nt;
     const int cls_nn = tnn < nt ? tile_class(tnn) : TILE_SKIP;
     if constexpr (PAGED) rows_n = tnn < nt ? tile_rows(tnn) : kNoRow;
@@ -449,7 +473,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int c = 0; c < 8; ++c) {
         const uint4 k0 = kf[c & 3][0], k1 = kf[c & 3][1];
         if (c + 4 < 8) { kf[c & 3][0] = kfrag(c + 4, 0); kf[c & 3][1] = kfrag(c + 4, 1); }
-        if (more) stage_part(st, tn, rows_tn, c);
+        if (more) stage_part(st, tn, rows_tn, first_tn, c);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int rg = 0; rg < kGroups; ++rg) {
