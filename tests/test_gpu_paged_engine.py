@@ -19,7 +19,7 @@ import torch
 from transformers import AutoModelForCausalLM, DynamicCache, Qwen3Config
 
 from oracle import prefill as opf
-from threadcut_amd import attention, kv, paged, workloads
+from threadcut_amd import attention, kv, paged, prefill, workloads
 from threadcut_amd.graph import DecodeGraph
 from threadcut_amd.match import Split, split
 
@@ -75,6 +75,32 @@ def test_paged_prefill_matches_oracle(gpu, g, page_tokens, n, q, mode):
     want = opf.prefill_f64(query.float().numpy(), k[None].float().numpy(), v[None].float().numpy(), SCALE,
                            mask=None if mask is None else mask.numpy(), causal=mode == "causal")
     assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-3
+
+
+@pytest.mark.parametrize("page_tokens", [64, 16])
+@pytest.mark.parametrize("q,mode", [(200, "causal"), (1000, "causal"), (300, "mask"), (64, "none")])
+def test_paged_prefill_bit_identical_to_contiguous(gpu, page_tokens, q, mode):
+    """The paged and the contiguous prefill run the same arithmetic and differ only in where a
+    row is read from. With 64-token pages filled in order every full 64-key tile is one page's
+    consecutive rows (addressed from its first offset), with 16-token pages every tile gathers
+    its rows through the per-token offsets, and the last, partial tile (1000 keys) gathers in
+    both: each must give the contiguous kernel's output bit for bit."""
+    n = 1000
+    cache, kvs = paged_with(gpu, 1, n, page_tokens, 41 + q)
+    gq = torch.Generator().manual_seed(q)
+    query = torch.randn(1, 32, q, 128, generator=gq).half().to(gpu)
+    mask = None
+    if mode == "mask":
+        vis = torch.rand(q, n, generator=gq) < 0.7
+        vis[:, -q:] &= torch.ones(q, q, dtype=torch.bool).tril()
+        mask = vis[None, None].to(gpu)
+    print(f"case: paged vs contiguous prefill P={page_tokens} q={q} {mode}", flush=True)
+    got = cache.prefill(0, query, SCALE, mask, causal=mode == "causal")
+    k, v = kvs[0]
+    want = prefill.prefill_attention(query, k[None].to(gpu), v[None].to(gpu), mask, SCALE,
+                                     is_causal=mode == "causal")
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
 @pytest.mark.parametrize("s", [Split(37, 100, 1000), Split(5, 600, 63), Split(0, 17, 500)])
