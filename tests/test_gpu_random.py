@@ -5,7 +5,10 @@ parity tests reach combinations the hand-picked cases do not.
 - Decode (tc_decode_attention through decode_attention_batched): batches with
   and without per-sequence lengths (empty sequences included), g in 1..8,
   fixed or tuned split lengths, against the float64 closed form
-  (threadcut/flash_decode.py:57-69): max-abs 2e-3 fp16, 4e-3 bf16.
+  (threadcut/flash_decode.py:57-69): max-abs 2e-3 fp16; bf16 4e-3 plus its
+  half-ulp of the value (2^-8 |x|), since a sequence of a few keys gives
+  outputs of 2 and more, where the bf16 rounding of the exact result alone
+  exceeds 4e-3.
 - Splice (tc_splice_rope through kv.splice): random (a, c0, c) on random
   capacities, overlapping and disjoint, against the oracle's restatement of
   threadcut/kv.py:83-92: bit-exact.
@@ -32,6 +35,12 @@ pytestmark = pytest.mark.gpu
 
 D = 128
 DECODE_TOL = {torch.float16: 2e-3, torch.bfloat16: 4e-3}
+DECODE_REL = {torch.float16: 0.0, torch.bfloat16: 2.0 ** -8}  # bf16: the half-ulp of the output value
+
+
+def decode_excess(out, want, dtype):
+    """Largest amount by which |out - want| exceeds the decode bound (<= 0 passes)."""
+    return float((np.abs(out - want) - (DECODE_TOL[dtype] + DECODE_REL[dtype] * np.abs(want))).max())
 PREFILL_TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
 
 
@@ -49,7 +58,8 @@ def decode_case(seed):
     return b, hkv, g, n, dtype, split, lens
 
 
-@pytest.mark.parametrize("seed", range(120))
+# Seed 237 (bf16, a sequence of 3 keys) gives outputs above 2, where bf16 rounds in steps of 2^-6.
+@pytest.mark.parametrize("seed", [*range(120), 237])
 def test_random_decode(gpu, seed):
     b, hkv, g, n, dtype, split, lens = decode_case(seed)
     print(f"case: decode seed={seed} B={b} Hkv={hkv} g={g} n={n} {dtype} split={split} "
@@ -64,7 +74,7 @@ def test_random_decode(gpu, seed):
     torch.cuda.synchronize()
     qn, kn, vn = q.float().numpy(), k.float().numpy(), v.float().numpy()
     want = od.attention_f64(qn, kn, vn, scale) if lens is None else od.decode_ragged(qn, kn, vn, lens.numpy(), scale)
-    assert np.abs(out.float().cpu().numpy() - want).max() <= DECODE_TOL[dtype]
+    assert decode_excess(out.float().cpu().numpy(), want, dtype) <= 0
 
 
 class _Cache:
@@ -189,7 +199,7 @@ def test_random_paged(gpu, seed):
     out = cache.decode(0, q.to(gpu), D ** -0.5)
     torch.cuda.synchronize()
     want = od.attention_f64(q.float().numpy(), keys, vals, D ** -0.5)
-    assert np.abs(out.float().cpu().numpy() - want).max() <= DECODE_TOL[dtype]
+    assert decode_excess(out.float().cpu().numpy(), want, dtype) <= 0
     nq = r.randint(1, min(cache.length(), 200)) if cache.length() else 0
     if nq:
         qp = torch.randn(1, nq, hkv * g, D, generator=gen).to(dtype).transpose(1, 2)
