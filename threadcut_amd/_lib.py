@@ -5,6 +5,7 @@ only way to reach the kernels: there is no fallback, and a missing library
 raises ``RuntimeError`` naming the build command.
 """
 import ctypes
+import functools
 import os
 import threading
 
@@ -122,8 +123,15 @@ def dtype_code(t):
         raise TypeError(f"threadcut_amd kernels take float16 or bfloat16 tensors, got {t}") from None
 
 
+@functools.lru_cache(maxsize=4096)
+def _i64x3(a, b, c):
+    return (ctypes.c_int64 * 3)(a, b, c)
+
+
 def i64x3(a, b, c):
-    return (ctypes.c_int64 * 3)(int(a), int(b), int(c))
+    """A C int64[3] of (a, b, c). The arrays are shared between calls with the same values (the
+    library only reads them), so a decode call does not build its stride arrays anew."""
+    return _i64x3(int(a), int(b), int(c))
 
 
 def i64x2(a, b):

@@ -10,6 +10,8 @@ log-sum-exp; a second kernel merges the splits with softmax(lse) weights
 ``libthreadcut_hip.so``; this module only checks tensors and passes pointers,
 strides and the current stream.
 """
+import functools
+
 import torch
 
 from . import _lib
@@ -81,6 +83,34 @@ def _strides3(t, token_dim=False):
     return _lib.i64x3(*st)
 
 
+@functools.lru_cache(maxsize=1024)
+def _plan(device_index, b, hkv, g, d, n, split, ragged):
+    """(splits, workspace bytes) of a call; the tuned plan depends on the device's compute units,
+    so it is computed with that device current."""
+    lib = _lib.load()
+    with torch.cuda.device(device_index):
+        s = num_splits(b, hkv, n, split, ragged)
+    return s, max(lib.tc_decode_workspace_bytes(b, hkv, g, d, s), 16)
+
+
+def _on_device(device):
+    """Context that makes `device` current, or nothing when it already is (the common case)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NO_SWITCH
+    return torch.cuda.device(device)
+
+
+class _NoSwitch:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_SWITCH = _NoSwitch()
+
+
 def decode_into(q, k, v, scale, out, lens=None, split=None):
     """out[b,h,g,:] = softmax(q[b,h,g]·k[b,h,:len_b]ᵀ·scale)·v[b,h,:len_b] (fp32 math).
 
@@ -99,10 +129,9 @@ def decode_into(q, k, v, scale, out, lens=None, split=None):
             raise ValueError("decode_attention: lens must be a contiguous int32 [B] tensor on the device")
     lib = _lib.load()
     dt = _lib.dtype_code(q.dtype)
-    with torch.cuda.device(q.device):
-        s = num_splits(b, hkv, n, split, ragged=lens is not None)
-        nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
-        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    _, nbytes = _plan(q.device.index, b, hkv, g, d, n, split, lens is not None)
+    with _on_device(q.device):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
         rc = lib.tc_decode_attention(
             q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k, True), v.data_ptr(), _strides3(v, True),
             lens.data_ptr() if lens is not None else None, n,
@@ -133,10 +162,9 @@ def decode_append_into(q, k_cache, v_cache, k_new, v_new, n, scale, out, split=N
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(3) != 1:
         raise ValueError("decode_append: out must match q")
     lib = _lib.load()
-    with torch.cuda.device(q.device):
-        s = num_splits(b, hkv, n, split)
-        nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
-        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    _, nbytes = _plan(q.device.index, b, hkv, g, d, int(n), split, False)
+    with _on_device(q.device):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
         st2 = lambda t: _lib.i64x2(t.stride(0) if t.shape[0] > 1 else 0, t.stride(1) if t.shape[1] > 1 else 0)
         rc = lib.tc_decode_append_attention(
             q.data_ptr(), _strides3(q), k_cache.data_ptr(), _strides3(k_cache, True), v_cache.data_ptr(),
@@ -171,10 +199,9 @@ def decode_append_at(q, k_cache, v_cache, k_new, v_new, pos, scale, out, split=N
         raise ValueError("decode_append_at: out must match q")
     cap = k_cache.shape[2]
     lib = _lib.load()
-    with torch.cuda.device(q.device):
-        s = num_splits(b, hkv, cap, split)
-        nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
-        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    _, nbytes = _plan(q.device.index, b, hkv, g, d, int(cap), split, False)
+    with _on_device(q.device):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
         st2 = lambda t: _lib.i64x2(t.stride(0) if t.shape[0] > 1 else 0, t.stride(1) if t.shape[1] > 1 else 0)
         rc = lib.tc_decode_append_attention_at(
             q.data_ptr(), _strides3(q), k_cache.data_ptr(), _strides3(k_cache, True), v_cache.data_ptr(),
