@@ -302,3 +302,19 @@ def test_write_step_then_decode_reads_the_new_rows(gpu):
             v = torch.cat((v, vn[layer][b].cpu()[:, None]), 1)
             want = closed_form(q[b:b + 1].cpu(), k[None], v[None])
             assert np.abs(out[b:b + 1].float().cpu().numpy() - want).max() <= TOL[torch.float16]
+
+
+def test_cache_made_on_the_current_device_takes_its_tensors(gpu):
+    """PagedKV(device="cuda") names the current device; it records the pools' own device, so
+    queries on that device (with its index) are accepted and decoded."""
+    cache = PagedKV(1, 8, 8, 16, device="cuda")
+    assert cache.device.index == torch.cuda.current_device()
+    k = torch.randn(8, 40, 128, generator=torch.Generator().manual_seed(70)).half()
+    v = torch.randn(8, 40, 128, generator=torch.Generator().manual_seed(71)).half()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    cache.append(0, [k.to(dev)], [v.to(dev)])
+    q = torch.randn(1, 8, 4, 128, generator=torch.Generator().manual_seed(72)).half()
+    out = cache.decode(0, q.to(dev), 128 ** -0.5)
+    torch.cuda.synchronize()
+    want = od.attention_f64(q.float().numpy(), k.float().numpy()[None], v.float().numpy()[None], 128 ** -0.5)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-3

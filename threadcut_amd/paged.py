@@ -35,7 +35,7 @@ from transformers import DynamicCache
 from transformers.cache_utils import DynamicLayer
 
 from . import _lib
-from .flash_decode import HEAD_DIM, num_splits
+from .flash_decode import HEAD_DIM, _on_device, _plan
 from .kv import rope_table
 
 TILE = 16  # rows per tile-table entry (the decode kernel's tile)
@@ -239,7 +239,9 @@ class PagedKV:
         self.v_pools = [torch.zeros(shape, dtype=dtype, device=dev) for _ in range(layers)]
         self.kv_heads = kv_heads
         self.dtype = dtype
-        self.device = dev
+        # The pools' own device, with its index ("cuda" alone names the current device).
+        self.device = self.k_pools[0].device if self.k_pools else torch.device(
+            "cuda", torch.cuda.current_device() if dev.index is None else dev.index)
         self._dev_table = None  # (version, table, tiles, max_tiles)
 
     @property
@@ -400,10 +402,9 @@ class PagedKV:
         tab, cnt, mt = self.device_table()
         lib = _lib.load()
         kp, vp = self.k_pools[layer], self.v_pools[layer]
-        with torch.cuda.device(q.device):
-            s = num_splits(b, hkv, TILE * mt, split, ragged=b > 1)
-            nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
-            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+        _, nbytes = _plan(q.device.index, b, hkv, g, d, TILE * mt, split, b > 1)
+        with _on_device(q.device):
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
             rc = lib.tc_decode_paged_attention(
                 q.data_ptr(), _lib.i64x3(*q.stride()[:3]), kp.data_ptr(), vp.data_ptr(), self._strides(),
                 kp.shape[0], kp.shape[2], tab.data_ptr(), cnt.data_ptr(), mt, b, hkv, g, d,
@@ -467,10 +468,9 @@ class PagedKV:
         tab, cnt, mt = self.device_table()
         lib = _lib.load()
         kp, vp = self.k_pools[layer], self.v_pools[layer]
-        with torch.cuda.device(q.device):
-            s = num_splits(b, hkv, TILE * mt, split, ragged=b > 1)
-            nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
-            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+        _, nbytes = _plan(q.device.index, b, hkv, g, d, TILE * mt, split, b > 1)
+        with _on_device(q.device):
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
             rc = lib.tc_decode_paged_append_attention(
                 q.data_ptr(), _lib.i64x3(*q.stride()[:3]), kp.data_ptr(), vp.data_ptr(), self._strides(),
                 kp.shape[0], kp.shape[2], tab.data_ptr(), cnt.data_ptr(), mt,
@@ -503,10 +503,9 @@ class PagedKV:
         off, pitch = self.device_offsets()
         lib = _lib.load()
         kp, vp = self.k_pools[layer], self.v_pools[layer]
-        with torch.cuda.device(self.device):
-            s = num_splits(b, hkv, TILE * mt, None, ragged=b > 1)
-            nbytes = lib.tc_decode_workspace_bytes(b, hkv, g, d, s)
-            ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+        _, nbytes = _plan(self.device.index, b, hkv, g, d, TILE * mt, None, b > 1)
+        with _on_device(self.device):
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
             rc = lib.tc_decode_paged_append_attention_at(
                 q.data_ptr(), _lib.i64x3(*q.stride()[:3]), kp.data_ptr(), vp.data_ptr(), self._strides(),
                 kp.shape[0], kp.shape[2], tab.data_ptr(), cnt.data_ptr(), mt, off.data_ptr(), pitch, lens.data_ptr(),
