@@ -221,3 +221,15 @@ def test_slab_layers_share_one_allocation_through_growth():
         assert layer.keys.shape == (1, 2, 2100, 16)
         assert torch.equal(layer.keys, torch.cat((k, k[:, :, :100]), 2))
         assert torch.equal(layer.values, torch.cat((v, v[:, :, :100]), 2))
+
+
+def test_decode_graph_refuses_a_model_on_another_attention():
+    """The captured decode step leaves each layer's new K/V row to the "threadcut" decode kernel;
+    a model switched to another attention would attend over an unwritten row, so DecodeGraph
+    refuses it before it touches the cache or a device."""
+    from threadcut_amd.graph import DecodeGraph
+
+    m = tiny_model()
+    m.set_attn_implementation("sdpa")
+    with pytest.raises(ValueError, match="set_attn_implementation"):
+        DecodeGraph(m, kv.new_cache(m.config), max_new_tokens=4)

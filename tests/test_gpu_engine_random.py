@@ -1,0 +1,165 @@
+"""Seeded random sweeps of the drop-in through transformers: the engine's loop
+(threadcut/engine.py:70-95: prefill, decode steps, a splice, more decode steps)
+on small random Qwen3 models with the registered "threadcut" attention and
+this package's caches, against the same model run with stock SDPA on a
+DynamicCache that is spliced by the oracle's torch restatement of
+threadcut/kv.py:83-92.
+
+Drawn per case: KV heads (1, 2, 4) and query heads per KV head (1, 2, 3, 4,
+6, 8: the decode kernels take every g <= 8, prefill falls back to the
+reference's repeat_kv + SDPA route for 3 and 6), batch 1 or 2, the cache kind
+(GrowingLayer with copying or fused appends, the one-allocation slab, the
+paged cache with fused or copying appends and 16/32/64-token pages), prompt
+length, a second prefill chunk (a causal chunk mask), the split (empty
+prefix, empty suffix and no gap included), and whether the steps after the
+splice run as a captured DecodeGraph.
+
+Checks: every step's logits within 3e-2 of stock SDPA (the reference's fp16
+tolerance for model-level checks); at the end, layer 0's cached keys and
+values (which depend on the token embeddings alone, so no attention rounding
+reaches them) bit-identical to the reference cache's, deeper layers within
+3e-2.
+"""
+import random
+
+import pytest
+import torch
+from transformers import AutoModelForCausalLM, DynamicCache, Qwen3Config
+
+from oracle import splice as osp
+from threadcut_amd import attention, kv, paged
+from threadcut_amd.graph import DecodeGraph
+from threadcut_amd.match import Split
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 3e-2
+KINDS = ("plain", "fused", "slab", "paged", "paged_copy")
+_MODELS = {}
+
+
+def model_for(dev, hkv, g):
+    key = (hkv, g)
+    if key not in _MODELS:
+        torch.manual_seed(100 * hkv + g)
+        cfg = Qwen3Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                          num_attention_heads=hkv * g, num_key_value_heads=hkv, head_dim=128,
+                          max_position_embeddings=4096, rope_theta=1e6)
+        m = AutoModelForCausalLM.from_config(cfg, dtype=torch.float16, attn_implementation=attention.NAME)
+        _MODELS[key] = m.to(dev).eval()
+    return _MODELS[key]
+
+
+def engine_case(seed):
+    r = random.Random(seed)
+    hkv = r.choice([1, 2, 4])
+    g = r.choice([1, 2, 3, 4, 6, 8])
+    kind = r.choice(KINDS)
+    b = r.choice([1, 1, 2])
+    n0 = r.choice([1, 7, 64, r.randint(2, 1200)])
+    cut = r.randint(1, n0 - 1) if n0 > 1 and r.random() < 0.5 else None
+    steps = r.randint(1, 3)
+    s = None
+    if r.random() < 0.75:
+        n = n0 + steps
+        c0 = r.choice([0, n, r.randint(0, n), r.randint(0, n), r.randint(0, n)])
+        a = r.choice([0, c0, r.randint(0, c0), r.randint(0, c0)])
+        c = r.choice([0, n - c0, r.randint(0, n - c0), r.randint(0, n - c0)])
+        s = Split(a, c0, c)
+    after = r.randint(1, 3)
+    graph = r.random() < 0.5
+    page_tokens = r.choice([16, 32, 64])
+    return hkv, g, kind, b, n0, cut, steps, s, after, graph, page_tokens
+
+
+def new_ours(m, kind, b, n_max, page_tokens):
+    if kind.startswith("paged"):
+        pages = b * (-(-n_max // page_tokens) + 2) + 4
+        return paged.new_paged_cache(m.config, num_pages=pages, page_tokens=page_tokens, batch=b,
+                                     fused_append=kind == "paged")
+    return kv.new_cache(m.config, fused_append=kind != "plain", slab=kind == "slab")
+
+
+def forward(m, ids, cache, impl):
+    """Logits [B, vocab] of the last position of ids [B][t]."""
+    m.set_attn_implementation(impl)
+    x = torch.tensor(ids, device=m.device)
+    return m(input_ids=x, past_key_values=cache, use_cache=True).logits[:, -1].float()
+
+
+def ref_splice(cache, s, inv_freq):
+    """The oracle's splice (threadcut/kv.py:83-92) of a stock DynamicCache, on host copies."""
+    ks = [l.keys.cpu() for l in cache.layers]
+    vs = [l.values.cpu() for l in cache.layers]
+    osp.splice_growing_torch(ks, vs, s.a, s.c0, s.c, inv_freq.cpu())
+    keep = s.a + s.c
+    for l, k, v in zip(cache.layers, ks, vs):
+        l.keys = k[..., :keep, :].contiguous().to(l.keys.device)
+        l.values = v[..., :keep, :].contiguous().to(l.values.device)
+
+
+def our_layer_kv(cache, i, b):
+    """Layer i's cached keys and values [B, Hkv, n, D] in logical order."""
+    state = paged.state_of(cache)
+    if state is not None:
+        pairs = [state.kv.gather(i, j) for j in range(b)]
+        return torch.stack([k for k, _ in pairs]), torch.stack([v for _, v in pairs])
+    layer = cache.layers[i]
+    layer.flush()
+    return layer.keys, layer.values
+
+
+def close(a, b):
+    return (a - b).abs().max().item() <= ATOL
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("seed", range(64))
+def test_random_engine_loop(gpu, seed):
+    hkv, g, kind, b, n0, cut, steps, s, after, graph, page_tokens = engine_case(seed)
+    print(f"case: engine seed={seed} Hkv={hkv} g={g} {kind} B={b} prompt={n0} cut={cut} steps={steps} "
+          f"split={s} after={after} graph={graph} page_tokens={page_tokens}", flush=True)
+    m = model_for(gpu, hkv, g)
+    inv = m.model.rotary_emb.inv_freq
+    gen = random.Random(7000 + seed)
+    seqs = [[gen.randrange(10, 500) for _ in range(n0 + steps + after)] for _ in range(b)]
+    ours = new_ours(m, kind, b, n0 + steps + after + 1, page_tokens)
+    ref = DynamicCache(config=m.config)
+
+    chunks = [(0, n0)] if cut is None else [(0, cut), (cut, n0)]
+    for lo, hi in chunks:
+        a = forward(m, [q[lo:hi] for q in seqs], ours, attention.NAME)
+        w = forward(m, [q[lo:hi] for q in seqs], ref, "sdpa")
+        assert close(a, w), f"prefill chunk [{lo}, {hi})"
+    for t in range(n0, n0 + steps):
+        a = forward(m, [[q[t]] for q in seqs], ours, attention.NAME)
+        w = forward(m, [[q[t]] for q in seqs], ref, "sdpa")
+        assert close(a, w), f"decode step at {t}"
+    if s is not None:
+        kv.splice(ours, s, inv)
+        ref_splice(ref, s, inv)
+        assert ours.get_seq_length() == ref.get_seq_length() == s.a + s.c
+    tail = range(n0 + steps, n0 + steps + after)
+    if graph:
+        m.set_attn_implementation(attention.NAME)  # the reference's forward left the model on SDPA
+        dg = DecodeGraph(m, ours, max_new_tokens=after, batch=b)
+        for t in tail:
+            a = dg.step([q[t] for q in seqs]).float().clone()
+            w = forward(m, [[q[t]] for q in seqs], ref, "sdpa")
+            assert close(a, w), f"captured step at {t}"
+        dg.close()
+    else:
+        for t in tail:
+            a = forward(m, [[q[t]] for q in seqs], ours, attention.NAME)
+            w = forward(m, [[q[t]] for q in seqs], ref, "sdpa")
+            assert close(a, w), f"decode step at {t}"
+    torch.cuda.synchronize()
+    n = ref.get_seq_length()
+    assert ours.get_seq_length() == n
+    for i, rl in enumerate(ref.layers):
+        k, v = our_layer_kv(ours, i, b)
+        assert k.shape == rl.keys.shape == (b, hkv, n, 128)
+        if i == 0:
+            assert torch.equal(k, rl.keys) and torch.equal(v, rl.values)
+        else:
+            assert close(k.float(), rl.keys.float()) and close(v.float(), rl.values.float())

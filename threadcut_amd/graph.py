@@ -23,6 +23,10 @@ The host keeps each layer's token count in step (``n``) so that the cache is
 an ordinary cache again after ``close()``: splice, prefill and eager decode
 work on it as before.
 
+The model must run the "threadcut" attention: each layer's new K/V row is
+written by its decode kernel, and another attention would read the row
+unwritten, so DecodeGraph refuses a model set to any other.
+
 Two cache kinds are captured: ``kv.new_cache`` caches (GrowingLayer buffers,
 grown once to the step's capacity; the append position is a device counter)
 and ``paged.new_paged_cache`` caches (slots for the new tokens reserved ahead
@@ -31,7 +35,7 @@ sequence lengths are the device counter).
 """
 import torch
 
-from . import kv, paged
+from . import attention, kv, paged
 
 
 class _GrowingCache:
@@ -146,6 +150,12 @@ class DecodeGraph:
         types = set(getattr(model.config, "layer_types", None) or ["full_attention"])
         if types != {"full_attention"}:
             raise ValueError(f"DecodeGraph: layer types {sorted(types)}; only full-attention models are captured")
+        impl = getattr(model.config, "_attn_implementation", None)
+        if impl != attention.NAME:
+            # The captured step leaves each layer's new K/V row to the attention kernel,
+            # which writes it while it attends; any other attention would read a stale row.
+            raise ValueError(f"DecodeGraph: the model runs the {impl!r} attention; call "
+                             f"model.set_attn_implementation({attention.NAME!r}) first")
         self.store = (_PagedCache if paged.state_of(cache) is not None else _GrowingCache)(cache, batch,
                                                                                           max_new_tokens)
         dev = self.store.device

@@ -37,6 +37,7 @@ from transformers.cache_utils import DynamicLayer
 from . import _lib
 from .flash_decode import HEAD_DIM, _on_device, _plan
 from .kv import rope_table
+from .prefill import GROUPS
 
 TILE = 16  # rows per tile-table entry (the decode kernel's tile)
 _I64P = ctypes.POINTER(ctypes.c_int64)
@@ -718,9 +719,9 @@ def attention(layer, query, attention_mask, scaling):
     layer.flush()
     is_causal = attention_mask is None and q > 1 and q == layer.n
     m = attention_mask
-    if m is None or (m.dtype == torch.bool and m.dim() == 4 and m.shape[1] == 1):
+    if g in GROUPS and (m is None or (m.dtype == torch.bool and m.dim() == 4 and m.shape[1] == 1)):
         return kv.prefill(layer.index, query, scaling, m, is_causal)
-    # Other masks: the reference's route (repeat_kv + SDPA) on the gathered keys.
+    # Other masks and group sizes: the reference's route (repeat_kv + SDPA) on the gathered keys.
     ks, vs = zip(*[kv.gather(layer.index, i) for i in range(b)])
     k, v = torch.stack(ks), torch.stack(vs)
     out = F.scaled_dot_product_attention(query, k.repeat_interleave(g, 1), v.repeat_interleave(g, 1),
