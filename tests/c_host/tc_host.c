@@ -1,0 +1,161 @@
+/* A host program with no Python and no torch that drives the HIP path through
+ * the C ABI alone, as a cgo / JNI / N-API binding would: device buffers from
+ * hipMalloc, inputs from raw little-endian files, one call per entry point,
+ * outputs back to raw files. tests/test_gpu_c_host.py writes the inputs and
+ * checks the outputs.
+ *
+ *   tc_host decode DIR   meta.txt: B Hkv G N D scale split dtype
+ *                        q.bin [B,Hkv,G,D], k.bin / v.bin [B,Hkv,N,D] (2-byte elements)
+ *                        -> out.bin (tc_decode_attention, workspace from hipMalloc)
+ *                           out_noalloc.bin (tc_decode_attention_noalloc)
+ *   tc_host splice DIR   meta.txt: L B H cap D a c0 c dtype
+ *                        k.bin / v.bin [L,B,H,cap,D], table.bin (D fp32: cos ++ sin)
+ *                        -> k_out.bin / v_out.bin (tc_splice_rope over the L layers)
+ *
+ * Exit status: 0 done, 1 usage or file error, 2 HIP error, 3 the ABI refused
+ * the call (its message on stderr). */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "threadcut_hip.h"
+
+static char dir_buf[4096];
+
+static const char* path_in(const char* dir, const char* name) {
+  snprintf(dir_buf, sizeof dir_buf, "%s/%s", dir, name);
+  return dir_buf;
+}
+
+static void* read_file(const char* dir, const char* name, size_t bytes) {
+  FILE* f = fopen(path_in(dir, name), "rb");
+  void* p = malloc(bytes ? bytes : 1);
+  if (!f || !p || fread(p, 1, bytes, f) != bytes) {
+    fprintf(stderr, "tc_host: cannot read %zu bytes from %s\n", bytes, path_in(dir, name));
+    exit(1);
+  }
+  fclose(f);
+  return p;
+}
+
+static void write_file(const char* dir, const char* name, const void* p, size_t bytes) {
+  FILE* f = fopen(path_in(dir, name), "wb");
+  if (!f || fwrite(p, 1, bytes, f) != bytes) {
+    fprintf(stderr, "tc_host: cannot write %s\n", path_in(dir, name));
+    exit(1);
+  }
+  fclose(f);
+}
+
+static void hip_ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    fprintf(stderr, "tc_host: %s: %s\n", what, hipGetErrorString(e));
+    exit(2);
+  }
+}
+
+static void abi_ok(int rc, const char* what) {
+  if (rc != TC_OK) {
+    fprintf(stderr, "tc_host: %s: %s (%s)\n", what, tc_strerror(rc), tc_last_error());
+    exit(3);
+  }
+}
+
+/* A device buffer of `bytes`, filled from `host` unless that is NULL. */
+static void* to_device(const void* host, size_t bytes) {
+  void* d = NULL;
+  hip_ok(hipMalloc(&d, bytes ? bytes : 16), "hipMalloc");
+  if (host && bytes) hip_ok(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  return d;
+}
+
+static int decode(const char* dir) {
+  int b, hkv, g, d, split, dtype;
+  long long n;
+  float scale;
+  FILE* m = fopen(path_in(dir, "meta.txt"), "r");
+  if (!m || fscanf(m, "%d %d %d %lld %d %f %d %d", &b, &hkv, &g, &n, &d, &scale, &split, &dtype) != 8) {
+    fprintf(stderr, "tc_host: bad meta.txt\n");
+    return 1;
+  }
+  fclose(m);
+  const size_t q_bytes = (size_t)b * hkv * g * d * 2, kv_bytes = (size_t)b * hkv * (size_t)n * d * 2;
+  void* q = read_file(dir, "q.bin", q_bytes);
+  void* k = read_file(dir, "k.bin", kv_bytes);
+  void* v = read_file(dir, "v.bin", kv_bytes);
+  void *qd = to_device(q, q_bytes), *kd = to_device(k, kv_bytes), *vd = to_device(v, kv_bytes);
+  void *od = to_device(NULL, q_bytes), *od2 = to_device(NULL, q_bytes);
+  const int64_t qs[3] = {(int64_t)hkv * g * d, (int64_t)g * d, d};
+  const int64_t ks[3] = {(int64_t)hkv * n * d, (int64_t)n * d, d};
+
+  /* The caller sizes the workspace with the library's own split arithmetic. */
+  const int splits = tc_decode_num_splits(b, hkv, n, split, 0);
+  if (splits < 0) abi_ok(-splits, "tc_decode_num_splits");
+  const size_t ws_bytes = tc_decode_workspace_bytes(b, hkv, g, d, splits);
+  void* ws = to_device(NULL, ws_bytes);
+  abi_ok(tc_decode_attention(qd, qs, kd, ks, vd, ks, NULL, n, b, hkv, g, d, dtype, scale, split, ws, ws_bytes,
+                             od, qs, NULL),
+         "tc_decode_attention");
+  abi_ok(tc_decode_attention_noalloc(qd, qs, kd, ks, vd, ks, NULL, n, b, hkv, g, d, dtype, scale, split, od2, qs,
+                                     NULL),
+         "tc_decode_attention_noalloc");
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+
+  void* out = malloc(q_bytes);
+  hip_ok(hipMemcpy(out, od, q_bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  write_file(dir, "out.bin", out, q_bytes);
+  hip_ok(hipMemcpy(out, od2, q_bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  write_file(dir, "out_noalloc.bin", out, q_bytes);
+  printf("decode B=%d Hkv=%d G=%d N=%lld splits=%d workspace=%zu\n", b, hkv, g, n, splits, ws_bytes);
+  hipFree(qd); hipFree(kd); hipFree(vd); hipFree(od); hipFree(od2); hipFree(ws);
+  free(q); free(k); free(v); free(out);
+  return 0;
+}
+
+static int splice(const char* dir) {
+  int layers, b, h, d, dtype;
+  long long cap, a, c0, c;
+  FILE* m = fopen(path_in(dir, "meta.txt"), "r");
+  if (!m || fscanf(m, "%d %d %d %lld %d %lld %lld %lld %d", &layers, &b, &h, &cap, &d, &a, &c0, &c, &dtype) != 9 ||
+      layers < 1 || layers > 64) {
+    fprintf(stderr, "tc_host: bad meta.txt\n");
+    return 1;
+  }
+  fclose(m);
+  const size_t layer_elems = (size_t)b * h * (size_t)cap * d, bytes = layer_elems * 2 * layers;
+  void* k = read_file(dir, "k.bin", bytes);
+  void* v = read_file(dir, "v.bin", bytes);
+  float* table = read_file(dir, "table.bin", (size_t)d * sizeof(float));
+  char *kd = to_device(k, bytes), *vd = to_device(v, bytes);
+  void* kp[64];
+  void* vp[64];
+  for (int l = 0; l < layers; ++l) {
+    kp[l] = kd + (size_t)l * layer_elems * 2;
+    vp[l] = vd + (size_t)l * layer_elems * 2;
+  }
+  const int64_t st[3] = {(int64_t)h * cap * d, (int64_t)cap * d, d};
+  abi_ok(tc_splice_rope(kp, vp, layers, st, b, h, cap, d, dtype, a, c0, c, table, NULL), "tc_splice_rope");
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  hip_ok(hipMemcpy(k, kd, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  hip_ok(hipMemcpy(v, vd, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  write_file(dir, "k_out.bin", k, bytes);
+  write_file(dir, "v_out.bin", v, bytes);
+  printf("splice L=%d B=%d H=%d cap=%lld a=%lld c0=%lld c=%lld\n", layers, b, h, cap, a, c0, c);
+  hipFree(kd); hipFree(vd);
+  free(k); free(v); free(table);
+  return 0;
+}
+
+int main(int argc, char** argv) {
+  if (argc != 3) {
+    fprintf(stderr, "usage: tc_host decode|splice DIR\n");
+    return 1;
+  }
+  setvbuf(stdout, NULL, _IONBF, 0);
+  if (!strcmp(argv[1], "decode")) return decode(argv[2]);
+  if (!strcmp(argv[1], "splice")) return splice(argv[2]);
+  fprintf(stderr, "tc_host: unknown mode %s\n", argv[1]);
+  return 1;
+}

@@ -58,3 +58,14 @@ def test_c_program_uses_the_abi(tmp_path):
     assert tuple(r) == (4, 7, 4)
     assert out[4] == "split rc 0 a 4 c0 7 c 4"
     assert out[5] == f"bad strides rc {_lib.TC_ERR_ALIGNMENT} msg set"
+
+
+def test_c_host_program_is_built():
+    """tests/c_host/tc_host (built with the library) links against it and the HIP runtime and
+    rejects a bad command line before any HIP call; the GPU tests run it on the device."""
+    host = os.path.join(ROOT, "tests", "c_host", "tc_host")
+    assert os.access(host, os.X_OK), "run python -m threadcut_amd.build"
+    r = subprocess.run([host], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "usage" in r.stderr
+    r = subprocess.run([host, "decode", "/nonexistent"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "meta.txt" in r.stderr

@@ -1,0 +1,141 @@
+"""The HIP path driven from a plain C host program (tests/c_host/tc_host.c,
+built with the library by threadcut_amd.build): device buffers from hipMalloc,
+the C ABI's entry points, no Python or torch in that process, as a cgo / JNI /
+N-API binding would drive it.
+
+- Decode (tc_decode_attention with a hipMalloc workspace, and
+  tc_decode_attention_noalloc): the golden fixtures against their float64
+  outputs within 2e-3, and random fp16 / bf16 batches against the float64
+  closed form of threadcut/flash_decode.py:57-69 (2e-3 fp16; bf16 4e-3 plus
+  its half-ulp 2^-8 |x|). Both entry points bit-identical to each other and to
+  the same call made through the Python wrapper in this process.
+- Splice (tc_splice_rope over L layers): the golden fixtures and random
+  multi-layer overlapping, short-gap and disjoint moves, bit-exact against the
+  oracle's restatement of threadcut/kv.py:83-92.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+from oracle import splice as osp
+from threadcut_amd import flash_decode
+from threadcut_amd.match import Split
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HOST = os.path.join(ROOT, "tests", "c_host", "tc_host")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+D = 128
+DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1}
+
+
+def run_host(mode, d):
+    if not os.access(HOST, os.X_OK):
+        pytest.fail("tests/c_host/tc_host is not built: run python -m threadcut_amd.build")
+    print(f"case: tc_host {mode} {d}", flush=True)
+    r = subprocess.run([HOST, mode, str(d)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, f"tc_host exited {r.returncode}: {r.stderr}"
+    return r.stdout
+
+
+def bits(t):
+    """A 2-byte CPU tensor's raw bytes."""
+    return t.contiguous().view(torch.int16).numpy().tobytes()
+
+
+def from_bits(raw, shape, dtype):
+    return torch.from_numpy(np.frombuffer(raw, dtype=np.int16).copy()).view(dtype).reshape(shape)
+
+
+def host_decode(tmp, q, k, v, scale, split, dtype):
+    """q [B, Hkv, G, D], k/v [B, Hkv, N, D] CPU tensors -> (out, out_noalloc) from the C host."""
+    b, hkv, g, _ = q.shape
+    n = k.shape[2]
+    (tmp / "q.bin").write_bytes(bits(q))
+    (tmp / "k.bin").write_bytes(bits(k))
+    (tmp / "v.bin").write_bytes(bits(v))
+    (tmp / "meta.txt").write_text(f"{b} {hkv} {g} {n} {D} {scale!r} {split} {DTYPE_CODE[dtype]}\n")
+    run_host("decode", tmp)
+    return (from_bits((tmp / "out.bin").read_bytes(), q.shape, dtype),
+            from_bits((tmp / "out_noalloc.bin").read_bytes(), q.shape, dtype))
+
+
+@pytest.mark.parametrize("name", ["decode_g4_n300.npz", "decode_g2_n77.npz"])
+def test_c_host_decode_reproduces_fixture(gpu, tmp_path, name):
+    f = np.load(os.path.join(GOLDEN, name))
+    q, k, v = (torch.from_numpy(f[x])[None] for x in ("q", "k", "v"))
+    scale = float(np.float32(f["scale"]))
+    out, out_na = host_decode(tmp_path, q, k, v, scale, 256, torch.float16)
+    assert np.abs(out[0].float().numpy() - f["out64"]).max() <= 2e-3
+    assert torch.equal(out.view(torch.int16), out_na.view(torch.int16))
+    py = flash_decode.decode_attention_batched(q.to(gpu), k.to(gpu), v.to(gpu), scale, split=256)
+    assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b,hkv,g,n,split", [(1, 8, 4, 10240, 0), (2, 8, 4, 3000, 256), (3, 2, 8, 777, 64),
+                                             (1, 4, 1, 1, 0), (2, 1, 5, 4097, 0)])
+def test_c_host_decode_matches_closed_form(gpu, tmp_path, dtype, b, hkv, g, n, split):
+    gen = torch.Generator().manual_seed(n + 7 * g)
+    q = torch.randn(b, hkv, g, D, generator=gen).to(dtype)
+    k = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    v = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    scale = D ** -0.5
+    out, out_na = host_decode(tmp_path, q, k, v, scale, split, dtype)
+    want = od.attention_f64(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale)
+    tol, rel = (2e-3, 0.0) if dtype == torch.float16 else (4e-3, 2.0 ** -8)
+    assert (np.abs(out.float().numpy() - want) - (tol + rel * np.abs(want))).max() <= 0
+    assert torch.equal(out.view(torch.int16), out_na.view(torch.int16))
+    py = flash_decode.decode_attention_batched(q.to(gpu), k.to(gpu), v.to(gpu), scale, split=split or None)
+    assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
+
+
+def host_splice(tmp, ks, vs, s, cos, sin, dtype):
+    """ks/vs [L, B, H, cap, D] CPU tensors -> spliced (ks, vs) from the C host."""
+    layers, b, h, cap, _ = ks.shape
+    (tmp / "k.bin").write_bytes(bits(ks))
+    (tmp / "v.bin").write_bytes(bits(vs))
+    (tmp / "table.bin").write_bytes(np.concatenate((cos, sin)).astype(np.float32).tobytes())
+    (tmp / "meta.txt").write_text(f"{layers} {b} {h} {cap} {D} {s.a} {s.c0} {s.c} {DTYPE_CODE[dtype]}\n")
+    run_host("splice", tmp)
+    return (from_bits((tmp / "k_out.bin").read_bytes(), ks.shape, dtype),
+            from_bits((tmp / "v_out.bin").read_bytes(), vs.shape, dtype))
+
+
+@pytest.mark.parametrize("name", ["splice_overlap_n40.npz", "splice_gap_n96.npz"])
+def test_c_host_splice_reproduces_fixture(gpu, tmp_path, name):
+    f = np.load(os.path.join(GOLDEN, name))
+    s = Split(*(int(x) for x in f["split"]))
+    ks, vs = torch.from_numpy(f["k"])[None], torch.from_numpy(f["v"])[None]
+    k_out, v_out = host_splice(tmp_path, ks, vs, s, f["cos"], f["sin"], torch.float16)
+    assert np.array_equal(k_out[0].numpy().view(np.uint16), f["k_out"].view(np.uint16))
+    assert np.array_equal(v_out[0].numpy().view(np.uint16), f["v_out"].view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layers,b,h,cap,s", [
+    (3, 2, 4, 300, Split(37, 58, 200)),     # overlapping, gap 21: the strip walk
+    (2, 1, 8, 700, Split(10, 150, 500)),    # overlapping, gap 140: chain walks
+    (4, 1, 2, 400, Split(5, 250, 120)),     # disjoint
+    (1, 1, 1, 64, Split(0, 1, 63)),         # gap 1 over the whole buffer
+])
+def test_c_host_splice_matches_oracle(gpu, tmp_path, dtype, layers, b, h, cap, s):
+    gen = torch.Generator().manual_seed(cap + s.c0)
+    ks = torch.randn(layers, b, h, cap, D, generator=gen).to(dtype)
+    vs = torch.randn(layers, b, h, cap, D, generator=gen).to(dtype)
+    inv = osp.default_inv_freq(1e6, D)
+    cos, sin = osp.rope_table(-s.gap, inv)
+    k_out, v_out = host_splice(tmp_path, ks, vs, s, cos, sin, dtype)
+    name = "float16" if dtype == torch.float16 else "bfloat16"
+    for l in range(layers):
+        k_in = ks[l].view(torch.int16).numpy().view(np.uint16) if dtype == torch.bfloat16 else ks[l].numpy()
+        v_in = vs[l].view(torch.int16).numpy().view(np.uint16) if dtype == torch.bfloat16 else vs[l].numpy()
+        kw, vw, n = osp.splice_growing(k_in, v_in, cap, s.a, s.c0, s.c, cos, sin, dtype=name)
+        assert n == s.a + s.c
+        assert np.array_equal(k_out[l].view(torch.int16).numpy().view(np.uint16), kw.view(np.uint16))
+        assert np.array_equal(v_out[l].view(torch.int16).numpy().view(np.uint16), vw.view(np.uint16))

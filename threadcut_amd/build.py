@@ -5,6 +5,8 @@ Compiles every ``csrc/*.hip`` source with hipcc (and the host-only
 ``libthreadcut_hip.so`` next to this file, where
 ``threadcut_amd._lib`` loads it. The measurement kernels of ``csrc/bench/``
 (not part of the decode ABI) link into ``libthreadcut_bench.so`` beside it.
+When the repository's ``tests/c_host/tc_host.c`` is present, it is built too
+(gcc, C99): a host program that drives the library through the C ABI alone.
 Run as ``python -m threadcut_amd.build``.
 """
 import concurrent.futures
@@ -20,6 +22,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libthreadcut_hip.so")
 BENCH_LIB = os.path.join(HERE, "libthreadcut_bench.so")
 ARCH = "gfx950"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+C_HOST = os.path.join(os.path.dirname(HERE), "tests", "c_host", "tc_host.c")
 
 # Packed-fp32 VALU forms stay off: the kernels are written for scalar fp32.
 COMMON_FLAGS = [
@@ -72,7 +76,22 @@ def build(verbose=False):
                 print(f"[{os.path.basename(src)}]\n{warn}", file=sys.stderr)
     _link(objs[:len(sources)], LIB)
     _link(objs[len(sources):], BENCH_LIB)
+    if os.path.exists(C_HOST):
+        _build_c_host(C_HOST, os.path.splitext(C_HOST)[0])
     return LIB
+
+
+def _build_c_host(src, out):
+    """A C99 program linked against the library and the HIP runtime, as a non-Python host
+    (cgo, JNI, N-API) would link; it finds the library next to this file at run time."""
+    rel = os.path.relpath(HERE, os.path.dirname(out))
+    cmd = ["gcc", "-std=c99", "-O2", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           f"-I{os.path.join(os.path.dirname(HERE), 'include')}", f"-I{ROCM}/include", src,
+           f"-L{HERE}", "-lthreadcut_hip", f"-L{ROCM}/lib", "-lamdhip64",
+           f"-Wl,-rpath,$ORIGIN/{rel}", f"-Wl,-rpath,{ROCM}/lib", "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"gcc failed on {os.path.basename(src)}:\n{r.stderr}")
 
 
 if __name__ == "__main__":
