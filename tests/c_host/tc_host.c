@@ -8,6 +8,10 @@
  *                        q.bin [B,Hkv,G,D], k.bin / v.bin [B,Hkv,N,D] (2-byte elements)
  *                        -> out.bin (tc_decode_attention, workspace from hipMalloc)
  *                           out_noalloc.bin (tc_decode_attention_noalloc)
+ *   tc_host prefill DIR  meta.txt: B Hq Hkv Q N D scale causal mask_batch dtype
+ *                        q.bin [B,Hq,Q,D], k.bin / v.bin [B,Hkv,N,D], mask.bin [mask_batch,Q,N]
+ *                        bytes when mask_batch > 0 (its tile map built with tc_prefill_mask_tiles)
+ *                        -> out.bin [B,Q,Hq,D] (tc_prefill_attention, splits chosen by the library)
  *   tc_host splice DIR   meta.txt: L B H cap D a c0 c dtype
  *                        k.bin / v.bin [L,B,H,cap,D], table.bin (D fp32: cos ++ sin)
  *                        -> k_out.bin / v_out.bin (tc_splice_rope over the L layers)
@@ -114,6 +118,60 @@ static int decode(const char* dir) {
   return 0;
 }
 
+static int prefill(const char* dir) {
+  int b, hq, hkv, d, causal, mb, dtype;
+  long long ql, n;
+  float scale;
+  FILE* m = fopen(path_in(dir, "meta.txt"), "r");
+  if (!m || fscanf(m, "%d %d %d %lld %lld %d %f %d %d %d", &b, &hq, &hkv, &ql, &n, &d, &scale, &causal, &mb,
+                   &dtype) != 10) {
+    fprintf(stderr, "tc_host: bad meta.txt\n");
+    return 1;
+  }
+  fclose(m);
+  const size_t q_bytes = (size_t)b * hq * (size_t)ql * d * 2, kv_bytes = (size_t)b * hkv * (size_t)n * d * 2;
+  void* q = read_file(dir, "q.bin", q_bytes);
+  void* k = read_file(dir, "k.bin", kv_bytes);
+  void* v = read_file(dir, "v.bin", kv_bytes);
+  void *qd = to_device(q, q_bytes), *kd = to_device(k, kv_bytes), *vd = to_device(v, kv_bytes);
+  void* od = to_device(NULL, q_bytes);
+  const int64_t qs[3] = {(int64_t)hq * ql * d, (int64_t)ql * d, d};
+  const int64_t ks[3] = {(int64_t)hkv * n * d, (int64_t)n * d, d};
+  const int64_t os[3] = {(int64_t)ql * hq * d, (int64_t)hq * d, d};
+
+  void *mask = NULL, *maskd = NULL, *tilesd = NULL;
+  size_t tiles_bytes = 0;
+  int64_t ms[3] = {0, 0, 1};
+  if (mb > 0) {
+    const size_t mask_bytes = (size_t)mb * (size_t)ql * (size_t)n;
+    mask = read_file(dir, "mask.bin", mask_bytes);
+    maskd = to_device(mask, mask_bytes);
+    ms[0] = mb > 1 ? ql * n : 0;  /* one mask for every sequence: batch stride 0 */
+    ms[1] = n;
+    tiles_bytes = tc_prefill_tiles_bytes(ql, n, mb, hq, hkv);
+    if (!tiles_bytes) abi_ok(TC_ERR_INVALID_ARGUMENT, "tc_prefill_tiles_bytes");
+    tilesd = to_device(NULL, tiles_bytes);
+    abi_ok(tc_prefill_mask_tiles(maskd, ms, mb, ql, n, hq, hkv, tilesd, tiles_bytes, NULL), "tc_prefill_mask_tiles");
+  }
+  const int splits = tc_prefill_num_splits(b, ql, n, hq, hkv);
+  if (splits < 0) abi_ok(-splits, "tc_prefill_num_splits");
+  const size_t ws_bytes = tc_prefill_workspace_bytes(b, ql, hq, splits);
+  void* ws = to_device(NULL, ws_bytes);
+  abi_ok(tc_prefill_attention(qd, qs, kd, ks, vd, ks, maskd, ms, tilesd, tiles_bytes, causal, ql, n, b, hq, hkv, d,
+                              dtype, scale, splits, ws, ws_bytes, od, os, NULL),
+         "tc_prefill_attention");
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  void* out = malloc(q_bytes);
+  hip_ok(hipMemcpy(out, od, q_bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  write_file(dir, "out.bin", out, q_bytes);
+  printf("prefill B=%d Hq=%d Hkv=%d Q=%lld N=%lld splits=%d mask_batch=%d causal=%d\n", b, hq, hkv, ql, n, splits,
+         mb, causal);
+  hipFree(qd); hipFree(kd); hipFree(vd); hipFree(od); hipFree(ws);
+  if (maskd) { hipFree(maskd); hipFree(tilesd); free(mask); }
+  free(q); free(k); free(v); free(out);
+  return 0;
+}
+
 static int splice(const char* dir) {
   int layers, b, h, d, dtype;
   long long cap, a, c0, c;
@@ -150,11 +208,12 @@ static int splice(const char* dir) {
 
 int main(int argc, char** argv) {
   if (argc != 3) {
-    fprintf(stderr, "usage: tc_host decode|splice DIR\n");
+    fprintf(stderr, "usage: tc_host decode|prefill|splice DIR\n");
     return 1;
   }
   setvbuf(stdout, NULL, _IONBF, 0);
   if (!strcmp(argv[1], "decode")) return decode(argv[2]);
+  if (!strcmp(argv[1], "prefill")) return prefill(argv[2]);
   if (!strcmp(argv[1], "splice")) return splice(argv[2]);
   fprintf(stderr, "tc_host: unknown mode %s\n", argv[1]);
   return 1;

@@ -9,6 +9,10 @@ N-API binding would drive it.
   closed form of threadcut/flash_decode.py:57-69 (2e-3 fp16; bf16 4e-3 plus
   its half-ulp 2^-8 |x|). Both entry points bit-identical to each other and to
   the same call made through the Python wrapper in this process.
+- Prefill (tc_prefill_attention, with tc_prefill_mask_tiles for a mask): g in
+  1, 2, 4, 8, no mask, is_causal, broadcast and per-sequence boolean masks,
+  against the float64 closed form of threadcut/attention.py:43-46 (2e-3 fp16,
+  1.6e-2 bf16) and bit-identical to prefill.prefill_attention in this process.
 - Splice (tc_splice_rope over L layers): the golden fixtures and random
   multi-layer overlapping, short-gap and disjoint moves, bit-exact against the
   oracle's restatement of threadcut/kv.py:83-92.
@@ -21,8 +25,9 @@ import pytest
 import torch
 
 from oracle import decode as od
+from oracle import prefill as opf
 from oracle import splice as osp
-from threadcut_amd import flash_decode
+from threadcut_amd import flash_decode, prefill
 from threadcut_amd.match import Split
 
 pytestmark = pytest.mark.gpu
@@ -92,6 +97,41 @@ def test_c_host_decode_matches_closed_form(gpu, tmp_path, dtype, b, hkv, g, n, s
     assert (np.abs(out.float().numpy() - want) - (tol + rel * np.abs(want))).max() <= 0
     assert torch.equal(out.view(torch.int16), out_na.view(torch.int16))
     py = flash_decode.decode_attention_batched(q.to(gpu), k.to(gpu), v.to(gpu), scale, split=split or None)
+    assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("b,hq,hkv,ql,n,mode,dtype", [
+    (1, 32, 8, 300, 1000, "causal", torch.float16),
+    (2, 8, 8, 64, 64, "none", torch.bfloat16),
+    (2, 16, 2, 200, 700, "mask_per_sequence", torch.float16),
+    (1, 8, 4, 129, 2100, "mask_broadcast", torch.bfloat16),
+    (2, 32, 8, 512, 4096, "causal", torch.float16),
+])
+def test_c_host_prefill_matches_closed_form(gpu, tmp_path, b, hq, hkv, ql, n, mode, dtype):
+    gen = torch.Generator().manual_seed(ql + n)
+    q = torch.randn(b, hq, ql, D, generator=gen).to(dtype)
+    k = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    v = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    scale = D ** -0.5
+    mask = None
+    if mode.startswith("mask"):
+        mb = b if mode == "mask_per_sequence" else 1
+        chunk = torch.arange(n)[None, :] <= torch.arange(ql)[:, None] + (n - ql)
+        mask = (chunk & (torch.rand(mb, ql, n, generator=gen) < 0.8))[:, None]  # [mb, 1, Q, N]
+        (tmp_path / "mask.bin").write_bytes(mask[:, 0].to(torch.uint8).numpy().tobytes())
+    (tmp_path / "q.bin").write_bytes(bits(q))
+    (tmp_path / "k.bin").write_bytes(bits(k))
+    (tmp_path / "v.bin").write_bytes(bits(v))
+    (tmp_path / "meta.txt").write_text(f"{b} {hq} {hkv} {ql} {n} {D} {scale!r} {int(mode == 'causal')} "
+                                       f"{0 if mask is None else mask.shape[0]} {DTYPE_CODE[dtype]}\n")
+    run_host("prefill", tmp_path)
+    out = from_bits((tmp_path / "out.bin").read_bytes(), (b, ql, hq, D), dtype)
+    want = opf.prefill_f64(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale,
+                           None if mask is None else mask.numpy(), mode == "causal")
+    tol = 2e-3 if dtype == torch.float16 else 1.6e-2
+    assert np.abs(out.float().numpy() - want).max() <= tol
+    py = prefill.prefill_attention(q.to(gpu), k.to(gpu), v.to(gpu), None if mask is None else mask.to(gpu), scale,
+                                   mode == "causal")
     assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
 
 
