@@ -12,12 +12,22 @@
  *                        q.bin [B,Hq,Q,D], k.bin / v.bin [B,Hkv,N,D], mask.bin [mask_batch,Q,N]
  *                        bytes when mask_batch > 0 (its tile map built with tc_prefill_mask_tiles)
  *                        -> out.bin [B,Q,Hq,D] (tc_prefill_attention, splits chosen by the library)
+ *   tc_host paged DIR    meta.txt: Hkv G N D scale P pages a c0 c dtype
+ *                        q.bin [1,Hkv,G,D], k.bin / v.bin [Hkv,N,D] (one sequence, logical
+ *                        order), order.bin int64 [pages] (the order pages are handed out),
+ *                        table.bin (D fp32: cos ++ sin of the prune's -(c0 - a) rotation)
+ *                        -> tokens in pages order[t / P], slots t % P; when c0 > a a prune
+ *                           (tc_page_prune, tc_page_tiles, tc_paged_rotate_keys), then
+ *                           tc_decode_paged_attention over the kept tiles: out.bin
+ *                           [1,Hkv,G,D], k_pool.bin / v_pool.bin [pages,Hkv,P,D] and
+ *                           frags.bin int64 [F,3] (the sequence's fragments)
  *   tc_host splice DIR   meta.txt: L B H cap D a c0 c dtype
  *                        k.bin / v.bin [L,B,H,cap,D], table.bin (D fp32: cos ++ sin)
  *                        -> k_out.bin / v_out.bin (tc_splice_rope over the L layers)
  *
  * Exit status: 0 done, 1 usage or file error, 2 HIP error, 3 the ABI refused
  * the call (its message on stderr). */
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -172,6 +182,106 @@ static int prefill(const char* dir) {
   return 0;
 }
 
+static void* upload_tiles(const int64_t* frags, int64_t nf, int64_t* count) {
+  const int64_t nt = tc_page_tiles(frags, nf, 0, NULL, 0);
+  if (nt < 0) abi_ok((int)-nt, "tc_page_tiles");
+  int32_t* tiles = calloc((size_t)(nt ? nt : 1) * 4, sizeof(int32_t));
+  if (nt && tc_page_tiles(frags, nf, 0, tiles, nt) != nt) abi_ok(TC_ERR_INVALID_ARGUMENT, "tc_page_tiles");
+  void* d = to_device(tiles, (size_t)(nt ? nt : 1) * 4 * sizeof(int32_t));
+  free(tiles);
+  *count = nt;
+  return d;
+}
+
+static int paged(const char* dir) {
+  int hkv, g, d, pt, pages, dtype;
+  long long n, a, c0, c;
+  float scale;
+  FILE* m = fopen(path_in(dir, "meta.txt"), "r");
+  if (!m || fscanf(m, "%d %d %lld %d %f %d %d %lld %lld %lld %d", &hkv, &g, &n, &d, &scale, &pt, &pages, &a, &c0,
+                   &c, &dtype) != 11 || n < 1 || pt < 1 || (n + pt - 1) / pt > pages) {
+    fprintf(stderr, "tc_host: bad meta.txt\n");
+    return 1;
+  }
+  fclose(m);
+  const size_t q_bytes = (size_t)hkv * g * d * 2, seq_bytes = (size_t)hkv * (size_t)n * d * 2;
+  const size_t pool_elems = (size_t)pages * hkv * pt * d, row = (size_t)d;
+  uint16_t* q = read_file(dir, "q.bin", q_bytes);
+  uint16_t* k = read_file(dir, "k.bin", seq_bytes);
+  uint16_t* v = read_file(dir, "v.bin", seq_bytes);
+  int64_t* order = read_file(dir, "order.bin", (size_t)pages * sizeof(int64_t));
+
+  /* One fragment per page: tokens [i P, (i + 1) P) in page order[i], from slot 0. */
+  int64_t nf = (n + pt - 1) / pt;
+  int64_t* frags = malloc((size_t)(nf + 1) * 3 * sizeof(int64_t));
+  uint16_t* kpool = calloc(pool_elems, 2);
+  uint16_t* vpool = calloc(pool_elems, 2);
+  for (int64_t i = 0; i < nf; ++i) {
+    frags[3 * i] = order[i];
+    frags[3 * i + 1] = 0;
+    frags[3 * i + 2] = (i + 1) * pt <= n ? pt : n - i * pt;
+  }
+  for (int64_t t = 0; t < n; ++t)
+    for (int h = 0; h < hkv; ++h) {
+      const size_t dst = (((size_t)order[t / pt] * hkv + h) * pt + (size_t)(t % pt)) * row;
+      memcpy(kpool + dst, k + ((size_t)h * n + t) * row, row * 2);
+      memcpy(vpool + dst, v + ((size_t)h * n + t) * row, row * 2);
+    }
+  void* kd = to_device(kpool, pool_elems * 2);
+  void* vd = to_device(vpool, pool_elems * 2);
+  const int64_t ps[3] = {(int64_t)hkv * pt * d, (int64_t)pt * d, d};
+
+  if (c0 > a) {
+    int64_t* kept = malloc((size_t)(nf + 1) * 3 * sizeof(int64_t));
+    int64_t* suffix = malloc((size_t)nf * 3 * sizeof(int64_t));
+    int64_t* freed = malloc((size_t)nf * sizeof(int64_t));
+    int64_t counts[3];
+    abi_ok(tc_page_prune(frags, nf, a, c0, c, kept, suffix, freed, counts), "tc_page_prune");
+    int64_t nt = 0;
+    void* sd = upload_tiles(suffix, counts[1], &nt);
+    float* table = read_file(dir, "table.bin", (size_t)d * sizeof(float));
+    void* pools[1] = {kd};
+    abi_ok(tc_paged_rotate_keys(pools, 1, ps, pages, pt, sd, nt, hkv, d, dtype, table, NULL),
+           "tc_paged_rotate_keys");
+    hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    hipFree(sd);
+    free(table);
+    memcpy(frags, kept, (size_t)counts[0] * 3 * sizeof(int64_t));
+    nf = counts[0];
+    printf("prune a=%lld c0=%lld c=%lld: %lld fragments kept, %lld pages freed, %lld tiles rotated\n", a, c0, c,
+           (long long)counts[0], (long long)counts[2], (long long)nt);
+    free(kept); free(suffix); free(freed);
+  }
+
+  int64_t mt = 0;
+  void* tab = upload_tiles(frags, nf, &mt);
+  const int32_t cnt = (int32_t)mt;
+  void* cnt_d = to_device(&cnt, sizeof cnt);
+  if (mt < 1) mt = 1;  /* the table's width, as the library sizes it */
+  const int splits = tc_decode_num_splits(1, hkv, 16 * mt, 0, 0);
+  if (splits < 0) abi_ok(-splits, "tc_decode_num_splits");
+  const size_t ws_bytes = tc_decode_workspace_bytes(1, hkv, g, d, splits);
+  void* ws = to_device(NULL, ws_bytes);
+  void* qd = to_device(q, q_bytes);
+  void* od = to_device(NULL, q_bytes);
+  const int64_t qs[3] = {(int64_t)hkv * g * d, (int64_t)g * d, d};
+  abi_ok(tc_decode_paged_attention(qd, qs, kd, vd, ps, pages, pt, tab, cnt_d, mt, 1, hkv, g, d, dtype, scale, 0, ws,
+                                   ws_bytes, od, qs, NULL),
+         "tc_decode_paged_attention");
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  hip_ok(hipMemcpy(q, od, q_bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  write_file(dir, "out.bin", q, q_bytes);
+  hip_ok(hipMemcpy(kpool, kd, pool_elems * 2, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  hip_ok(hipMemcpy(vpool, vd, pool_elems * 2, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  write_file(dir, "k_pool.bin", kpool, pool_elems * 2);
+  write_file(dir, "v_pool.bin", vpool, pool_elems * 2);
+  write_file(dir, "frags.bin", frags, (size_t)nf * 3 * sizeof(int64_t));
+  printf("paged decode Hkv=%d G=%d tiles=%lld splits=%d\n", hkv, g, (long long)cnt, splits);
+  hipFree(kd); hipFree(vd); hipFree(tab); hipFree(cnt_d); hipFree(ws); hipFree(qd); hipFree(od);
+  free(q); free(k); free(v); free(order); free(frags); free(kpool); free(vpool);
+  return 0;
+}
+
 static int splice(const char* dir) {
   int layers, b, h, d, dtype;
   long long cap, a, c0, c;
@@ -208,12 +318,13 @@ static int splice(const char* dir) {
 
 int main(int argc, char** argv) {
   if (argc != 3) {
-    fprintf(stderr, "usage: tc_host decode|prefill|splice DIR\n");
+    fprintf(stderr, "usage: tc_host decode|prefill|paged|splice DIR\n");
     return 1;
   }
   setvbuf(stdout, NULL, _IONBF, 0);
   if (!strcmp(argv[1], "decode")) return decode(argv[2]);
   if (!strcmp(argv[1], "prefill")) return prefill(argv[2]);
+  if (!strcmp(argv[1], "paged")) return paged(argv[2]);
   if (!strcmp(argv[1], "splice")) return splice(argv[2]);
   fprintf(stderr, "tc_host: unknown mode %s\n", argv[1]);
   return 1;

@@ -13,6 +13,11 @@ N-API binding would drive it.
   1, 2, 4, 8, no mask, is_causal, broadcast and per-sequence boolean masks,
   against the float64 closed form of threadcut/attention.py:43-46 (2e-3 fp16,
   1.6e-2 bf16) and bit-identical to prefill.prefill_attention in this process.
+- The paged cache (tc_page_prune, tc_page_tiles, tc_paged_rotate_keys,
+  tc_decode_paged_attention) on one sequence in shuffled pages: the pools'
+  kept rows bit-exact against the oracle's splice of the logical sequence,
+  decode against the float64 closed form, both bit-identical to PagedKV in
+  this process given the same page order.
 - Splice (tc_splice_rope over L layers): the golden fixtures and random
   multi-layer overlapping, short-gap and disjoint moves, bit-exact against the
   oracle's restatement of threadcut/kv.py:83-92.
@@ -28,6 +33,7 @@ from oracle import decode as od
 from oracle import prefill as opf
 from oracle import splice as osp
 from threadcut_amd import flash_decode, prefill
+from threadcut_amd.paged import PagedKV
 from threadcut_amd.match import Split
 
 pytestmark = pytest.mark.gpu
@@ -133,6 +139,61 @@ def test_c_host_prefill_matches_closed_form(gpu, tmp_path, b, hq, hkv, ql, n, mo
     py = prefill.prefill_attention(q.to(gpu), k.to(gpu), v.to(gpu), None if mask is None else mask.to(gpu), scale,
                                    mode == "causal")
     assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hkv,g,n,pt,s", [
+    (8, 4, 1000, 64, Split(100, 400, 600)),
+    (2, 8, 333, 16, Split(10, 17, 300)),
+    (4, 1, 129, 32, None),
+    (1, 5, 2048, 32, Split(0, 2000, 48)),
+    (2, 2, 700, 64, Split(650, 700, 0)),
+])
+def test_c_host_paged_prune_and_decode(gpu, tmp_path, dtype, hkv, g, n, pt, s):
+    gen = torch.Generator().manual_seed(n + pt)
+    q = torch.randn(1, hkv, g, D, generator=gen).to(dtype)
+    k = torch.randn(hkv, n, D, generator=gen).to(dtype)
+    v = torch.randn(hkv, n, D, generator=gen).to(dtype)
+    pages = -(-n // pt) + 3
+    order = torch.randperm(pages, generator=gen)
+    scale = D ** -0.5
+    inv = osp.default_inv_freq(1e6, D)
+    a, c0, c = (n, n, 0) if s is None else (s.a, s.c0, s.c)
+    cos, sin = osp.rope_table(-(c0 - a), inv)
+    (tmp_path / "q.bin").write_bytes(bits(q))
+    (tmp_path / "k.bin").write_bytes(bits(k))
+    (tmp_path / "v.bin").write_bytes(bits(v))
+    (tmp_path / "order.bin").write_bytes(order.numpy().astype(np.int64).tobytes())
+    (tmp_path / "table.bin").write_bytes(np.concatenate((cos, sin)).astype(np.float32).tobytes())
+    (tmp_path / "meta.txt").write_text(f"{hkv} {g} {n} {D} {scale!r} {pt} {pages} {a} {c0} {c} "
+                                       f"{DTYPE_CODE[dtype]}\n")
+    run_host("paged", tmp_path)
+    out = from_bits((tmp_path / "out.bin").read_bytes(), q.shape, dtype)
+    kp = from_bits((tmp_path / "k_pool.bin").read_bytes(), (pages, hkv, pt, D), dtype)
+    vp = from_bits((tmp_path / "v_pool.bin").read_bytes(), (pages, hkv, pt, D), dtype)
+    frags = np.frombuffer((tmp_path / "frags.bin").read_bytes(), dtype=np.int64).reshape(-1, 3)
+    k_kept = torch.cat([kp[p, :, f:f + m] for p, f, m in frags], 1)
+    v_kept = torch.cat([vp[p, :, f:f + m] for p, f, m in frags], 1)
+
+    name = "float16" if dtype == torch.float16 else "bfloat16"
+    as_np = (lambda t: t.numpy()) if dtype == torch.float16 else (lambda t: t.view(torch.int16).numpy().view(np.uint16))
+    kw, vw = osp.splice_copy(as_np(k), as_np(v), a, c0, c, cos, sin, dtype=name)
+    assert np.array_equal(as_np(k_kept).view(np.uint16), kw.view(np.uint16))
+    assert np.array_equal(as_np(v_kept).view(np.uint16), vw.view(np.uint16))
+    want = od.attention_f64(q.float().numpy(), k_kept[None].float().numpy(), v_kept[None].float().numpy(), scale)
+    tol, rel = (2e-3, 0.0) if dtype == torch.float16 else (4e-3, 2.0 ** -8)
+    assert (np.abs(out.float().numpy() - want) - (tol + rel * np.abs(want))).max() <= 0
+
+    cache = PagedKV(1, hkv, pages, pt, batch=1, dtype=dtype, device=gpu)
+    cache.table.free = order.flip(0).tolist()  # pop() hands the pages out in `order`
+    cache.append(0, [k.to(gpu)], [v.to(gpu)])
+    if s is not None:
+        cache.prune(0, s, inv)
+    py = cache.decode(0, q.to(gpu), scale)
+    assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
+    kg, vg = cache.gather(0)
+    assert torch.equal(kg.cpu().view(torch.int16), k_kept.view(torch.int16))
+    assert torch.equal(vg.cpu().view(torch.int16), v_kept.view(torch.int16))
 
 
 def host_splice(tmp, ks, vs, s, cos, sin, dtype):
