@@ -1,6 +1,6 @@
 """Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
 
-CPU: the oracle still reproduces every stored output (regression of the checker).
+CPU: the oracle still reproduces every stored output (a regression test of the oracle).
 GPU: the HIP kernels reproduce them (decode within 2e-3, splice bit-exact).
 """
 import os
