@@ -14,6 +14,12 @@ length, a second prefill chunk (a causal chunk mask), the split (empty
 prefix, empty suffix and no gap included), and whether the steps after the
 splice run as a captured DecodeGraph; float16 or bfloat16 weights and cache.
 
+A second sweep runs left-padded batches (2-3 sequences of different prompt
+lengths, the padding hidden by the attention mask transformers builds from
+the 2-D padding mask), where the decode steps carry a mask and take the
+masked branch: prefill and decode steps against stock SDPA given the same
+mask.
+
 Checks: every step's logits within 3e-2 of stock SDPA (the reference's fp16
 tolerance for model-level checks, kept for bf16 too: the two runs differ only
 in the attention's summation order, far below it); at the end, layer 0's cached keys and
@@ -185,3 +191,53 @@ def test_random_engine_loop(gpu, seed):
             assert torch.equal(k, rl.keys) and torch.equal(v, rl.values)
         else:
             assert rows_close(k, rl.keys, dtype) and rows_close(v, rl.values, dtype)
+
+
+def padded_case(seed):
+    r = random.Random(50000 + seed)
+    hkv = r.choice([1, 2, 4])
+    g = r.choice([1, 2, 3, 4, 8])
+    kind = r.choice(KINDS)
+    b = r.choice([2, 3])
+    n0 = r.choice([9, 64, r.randint(2, 900)])
+    pads = [0] + [r.randint(0, n0 - 1) for _ in range(b - 1)]
+    steps = r.randint(1, 4)
+    page_tokens = r.choice([16, 32, 64])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    return hkv, g, kind, b, n0, pads, steps, page_tokens, dtype
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("seed", range(24))
+def test_random_padded_batch(gpu, seed):
+    hkv, g, kind, b, n0, pads, steps, page_tokens, dtype = padded_case(seed)
+    print(f"case: padded seed={seed} Hkv={hkv} g={g} {kind} B={b} prompt={n0} pads={pads} steps={steps} "
+          f"page_tokens={page_tokens} {dtype}", flush=True)
+    m = model_for(gpu, hkv, g, dtype)
+    gen = random.Random(9000 + seed)
+    ids = [[0] * p + [gen.randrange(10, 500) for _ in range(n0 + steps - p)] for p in pads]
+    pad_mask = torch.tensor([[0] * p + [1] * (n0 + steps - p) for p in pads], device=gpu)
+    ours = new_ours(m, kind, b, n0 + steps + 1, page_tokens)
+    ref = DynamicCache(config=m.config)
+
+    def step(cache, impl, lo, hi):
+        m.set_attn_implementation(impl)
+        x = torch.tensor([q[lo:hi] for q in ids], device=gpu)
+        out = m(input_ids=x, attention_mask=pad_mask[:, :hi], past_key_values=cache, use_cache=True)
+        return out.logits[:, -1].float()
+
+    for lo, hi in [(0, n0)] + [(t, t + 1) for t in range(n0, n0 + steps)]:
+        a = step(ours, attention.NAME, lo, hi)
+        w = step(ref, "sdpa", lo, hi)
+        assert close(a, w), f"tokens [{lo}, {hi})"
+    torch.cuda.synchronize()
+    n = ref.get_seq_length()
+    for i, rl in enumerate(ref.layers):
+        k, v = our_layer_kv(ours, i, b)
+        if i == 0:
+            assert torch.equal(k, rl.keys) and torch.equal(v, rl.values)
+        else:
+            # Rows of padding attend to nothing visible in either run; compare the real tokens' rows.
+            for j, p in enumerate(pads):
+                assert rows_close(k[j, :, p:n], rl.keys[j, :, p:n], dtype)
+                assert rows_close(v[j, :, p:n], rl.values[j, :, p:n], dtype)

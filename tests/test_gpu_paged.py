@@ -243,8 +243,9 @@ def test_fused_paged_append_matches_append_then_decode(gpu, lens, P, dt):
 
 
 def test_decode_and_prune_refused_while_a_step_is_pending(gpu):
-    """After reserve_step() the tile table holds each sequence's unwritten slot: decode() and
-    prune() refuse until every layer has run decode_append (or cancel_step() drops the slots)."""
+    """After reserve_step() the tile table holds each sequence's unwritten slot: decode() of a
+    layer refuses until that layer has run decode_append, prune() until every layer has (or
+    cancel_step() drops the slots)."""
     cache, host = filled(gpu, 2, [100, 40], 16, 71)
     g = torch.Generator(device=gpu)
     g.manual_seed(71)
@@ -268,9 +269,16 @@ def test_decode_and_prune_refused_while_a_step_is_pending(gpu):
         want = closed_form(q[b:b + 1].cpu(), k[None], v[None])
         assert np.abs(out[b:b + 1].float().cpu().numpy() - want).max() <= TOL[torch.float16]
     cache.reserve_step()
-    cache.decode_append(0, q, kn, kn, SCALE)
+    fused = cache.decode_append(0, q, kn, kn, SCALE)
     with pytest.raises(RuntimeError, match="incomplete"):
         cache.decode(1, q, SCALE)
+    with pytest.raises(RuntimeError, match="incomplete"):
+        cache.prune(0, Split(10, 20, 30), workloads.inv_freq())
+    with pytest.raises(RuntimeError, match="incomplete"):
+        cache.reserve_step()
+    again = cache.decode(0, q, SCALE)  # layer 0's row is written: it reads the new token from its slot
+    torch.cuda.synchronize()
+    assert (again.float() - fused.float()).abs().max().item() <= TOL[torch.float16]
     cache.decode_append(1, q, kn, kn, SCALE)
     cache.decode(1, q, SCALE)  # the step is complete
     cache.prune(0, Split(10, 20, 30), workloads.inv_freq())

@@ -314,7 +314,7 @@ class PagedKV:
         [B|1, 1, q, n]. Returns [B, q, Hq, D] (the reference's transposed output)."""
         from . import prefill as pf
 
-        self._refuse_during_step("prefill")
+        self._refuse_during_step("prefill", layer)
         _lib.require_gpu(query, what="PagedKV.prefill")
         b, hq, ql, d = query.shape
         lens = {self.table.length(i) for i in range(self.table.batch)}
@@ -359,14 +359,19 @@ class PagedKV:
             _lib.check(rc, "tc_prefill_paged_attention")
         return out
 
-    def _step_pending(self):
+    def _step_pending(self, layer=None):
         """True between reserve_step() and the last layer's decode_append of that step:
-        the tile table then includes slots no layer has written yet."""
+        the tile table then includes slots not every layer has written yet. With `layer`,
+        True only while that layer's own row of the step is unwritten."""
         step = getattr(self, "_step", None)
-        return step is not None and step[0] == self.table.version and bool(step[1])
+        if step is None or step[0] != self.table.version:
+            return False
+        return bool(step[1]) if layer is None else layer in step[1]
 
-    def _refuse_during_step(self, what):
-        if self._step_pending():
+    def _refuse_during_step(self, what, layer=None):
+        """Refuse a read of the tile table while the reserved step's slots are unwritten: in
+        every layer (layer None: prune, a new reservation), or in the layer to be read."""
+        if self._step_pending(layer):
             raise RuntimeError(f"PagedKV.{what}: a reserved decode step is incomplete; run decode_append for "
                                "every layer (or cancel_step()) first")
 
@@ -385,7 +390,7 @@ class PagedKV:
         q [B, Hkv, G, D] (G query heads per KV head, last dim contiguous) in the
         pools' dtype; returns out [B, Hkv, G, D]. Enqueued on the current stream.
         """
-        self._refuse_during_step("decode")
+        self._refuse_during_step("decode", layer)
         _lib.require_gpu(q, what="PagedKV.decode")
         b, hkv, g, d = q.shape
         if b != self.table.batch or hkv != self.kv_heads or d != HEAD_DIM or q.dtype != self.dtype:
