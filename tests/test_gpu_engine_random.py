@@ -14,6 +14,12 @@ length, a second prefill chunk (a causal chunk mask), the split (empty
 prefix, empty suffix and no gap included), and whether the steps after the
 splice run as a captured DecodeGraph; float16 or bfloat16 weights and cache.
 
+A third sweep runs the engine's turns (threadcut/engine.py:36-59 then
+:88-95, repeated): per turn a random split of the cache, the next prompt's
+new tokens prefilled in one or two chunks on top of the spliced cache (a
+causal chunk mask over a pruned, for the paged cache fragmented, sequence),
+then decode steps, eager or captured.
+
 A second sweep runs left-padded batches (2-3 sequences of different prompt
 lengths, the padding hidden by the attention mask transformers builds from
 the 2-D padding mask), where the decode steps carry a mask and take the
@@ -241,3 +247,80 @@ def test_random_padded_batch(gpu, seed):
             for j, p in enumerate(pads):
                 assert rows_close(k[j, :, p:n], rl.keys[j, :, p:n], dtype)
                 assert rows_close(v[j, :, p:n], rl.values[j, :, p:n], dtype)
+
+
+def turns_case(seed):
+    r = random.Random(80000 + seed)
+    hkv = r.choice([1, 2, 4, 8])
+    g = r.choice([1, 2, 4, 5, 8])
+    kind = r.choice(KINDS)
+    b = r.choice([1, 1, 2])
+    n0 = r.randint(1, 600)
+    turns = []
+    n = n0
+    for _ in range(r.randint(1, 3)):
+        c0 = r.randint(0, n)
+        a = r.randint(0, c0)
+        c = r.randint(0, n - c0)
+        new = r.randint(1, 300)
+        chunks = [new] if r.random() < 0.6 or new < 2 else [r.randint(1, new - 1)]
+        if sum(chunks) < new:
+            chunks.append(new - chunks[0])
+        steps = r.randint(1, 3)
+        turns.append((Split(a, c0, c), chunks, steps, r.random() < 0.4))
+        n = a + c + new + steps
+    page_tokens = r.choice([16, 32, 64])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    return hkv, g, kind, b, n0, turns, page_tokens, dtype
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("seed", range(32))
+def test_random_engine_turns(gpu, seed):
+    hkv, g, kind, b, n0, turns, page_tokens, dtype = turns_case(seed)
+    print(f"case: turns seed={seed} Hkv={hkv} g={g} {kind} B={b} prompt={n0} turns={turns} "
+          f"page_tokens={page_tokens} {dtype}", flush=True)
+    m = model_for(gpu, hkv, g, dtype)
+    inv = m.model.rotary_emb.inv_freq
+    gen = random.Random(11000 + seed)
+    fresh = lambda k: [[gen.randrange(10, 500) for _ in range(k)] for _ in range(b)]  # noqa: E731
+    total = n0 + sum(sum(ch) + st for _, ch, st, _ in turns)
+    ours = new_ours(m, kind, b, 2 * total + 1, page_tokens)
+    ref = DynamicCache(config=m.config)
+
+    def both(ids):
+        a = forward(m, ids, ours, attention.NAME)
+        w = forward(m, ids, ref, "sdpa")
+        return a, w
+
+    a, w = both(fresh(n0))
+    assert close(a, w), "prompt"
+    for i, (s, chunks, steps, graph) in enumerate(turns):
+        kv.splice(ours, s, inv)
+        ref_splice(ref, s, inv)
+        assert ours.get_seq_length() == ref.get_seq_length() == s.a + s.c
+        for j, k in enumerate(chunks):
+            a, w = both(fresh(k))
+            assert close(a, w), f"turn {i} chunk {j} ({k} tokens on {ref.get_seq_length() - k})"
+        toks = fresh(steps)
+        if graph:
+            m.set_attn_implementation(attention.NAME)
+            dg = DecodeGraph(m, ours, max_new_tokens=steps, batch=b)
+            for t in range(steps):
+                got = dg.step([q[t] for q in toks]).float().clone()
+                want = forward(m, [[q[t]] for q in toks], ref, "sdpa")
+                assert close(got, want), f"turn {i} captured step {t}"
+            dg.close()
+        else:
+            for t in range(steps):
+                a, w = both([[q[t]] for q in toks])
+                assert close(a, w), f"turn {i} step {t}"
+    torch.cuda.synchronize()
+    n = ref.get_seq_length()
+    assert ours.get_seq_length() == n
+    for i, rl in enumerate(ref.layers):
+        k, v = our_layer_kv(ours, i, b)
+        if i == 0:
+            assert torch.equal(k, rl.keys) and torch.equal(v, rl.values)
+        else:
+            assert rows_close(k, rl.keys, dtype) and rows_close(v, rl.values, dtype)
