@@ -18,7 +18,8 @@ A third sweep runs the engine's turns (threadcut/engine.py:36-59 then
 :88-95, repeated): per turn a random split of the cache, the next prompt's
 new tokens prefilled in one or two chunks on top of the spliced cache (a
 causal chunk mask over a pruned, for the paged cache fragmented, sequence),
-then decode steps, eager or captured.
+then decode steps, eager or captured; transformers' own DynamicCache (spliced
+by tc_splice_copy) is one of its cache kinds.
 
 A second sweep runs left-padded batches (2-3 sequences of different prompt
 lengths, the padding hidden by the attention mask transformers builds from
@@ -90,6 +91,8 @@ def engine_case(seed):
 
 
 def new_ours(m, kind, b, n_max, page_tokens):
+    if kind == "dynamic":  # transformers' own cache with the "threadcut" attention (tc_splice_copy splices it)
+        return DynamicCache(config=m.config)
     if kind.startswith("paged"):
         pages = b * (-(-n_max // page_tokens) + 2) + 4
         return paged.new_paged_cache(m.config, num_pages=pages, page_tokens=page_tokens, batch=b,
@@ -122,7 +125,8 @@ def our_layer_kv(cache, i, b):
         pairs = [state.kv.gather(i, j) for j in range(b)]
         return torch.stack([k for k, _ in pairs]), torch.stack([v for _, v in pairs])
     layer = cache.layers[i]
-    layer.flush()
+    if isinstance(layer, kv.GrowingLayer):
+        layer.flush()
     return layer.keys, layer.values
 
 
@@ -271,11 +275,14 @@ def turns_case(seed):
         n = a + c + new + steps
     page_tokens = r.choice([16, 32, 64])
     dtype = r.choice([torch.float16, torch.bfloat16])
+    if r.random() < 0.25:
+        kind = "dynamic"
+        turns = [(sp, ch, st, False) for sp, ch, st, _ in turns]
     return hkv, g, kind, b, n0, turns, page_tokens, dtype
 
 
 @torch.no_grad()
-@pytest.mark.parametrize("seed", range(32))
+@pytest.mark.parametrize("seed", range(40))
 def test_random_engine_turns(gpu, seed):
     hkv, g, kind, b, n0, turns, page_tokens, dtype = turns_case(seed)
     print(f"case: turns seed={seed} Hkv={hkv} g={g} {kind} B={b} prompt={n0} turns={turns} "
