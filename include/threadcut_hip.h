@@ -309,7 +309,8 @@ int tc_splice_rope(void* const* k_layers_host, void* const* v_layers_host, int n
 /* Out of place: for every layer, rows [0, a) of src are copied to rows
  * [0, a) of dst, and rows [c0, c0+c) of src to rows [a, a+c) of dst, keys
  * shifted. This is the index_select branch of threadcut/kv.py:34-41 for
- * caches whose layers are not preallocated buffers. dst must not alias src. */
+ * caches whose layers are not preallocated buffers. dst must not alias src.
+ * a + c == 0 keeps nothing: no pointer is needed and nothing is enqueued. */
 int tc_splice_copy(void* const* k_src_host, void* const* v_src_host,
                    const int64_t src_strides[3], int64_t src_tokens,
                    void* const* k_dst_host, void* const* v_dst_host,

@@ -130,6 +130,13 @@ def test_splice_validation(lib):
     # No gap or no suffix: nothing to move, nothing enqueued.
     assert splice(10, 10, 50) == _lib.TC_OK
     assert splice(10, 30, 0) == _lib.TC_OK
+    # A copy that keeps nothing (a = c = 0) needs no pointers: the new cache is empty.
+    rc = lib.tc_splice_copy(_lib.ptr_array([0]), _lib.ptr_array([0]), st, 5, _lib.ptr_array([0]),
+                            _lib.ptr_array([0]), st, 1, 1, 8, 128, 0, 0, 5, 0, None, None)
+    assert rc == _lib.TC_OK
+    rc = lib.tc_splice_copy(_lib.ptr_array([0]), _lib.ptr_array([0]), st, 5, _lib.ptr_array([0]),
+                            _lib.ptr_array([0]), st, 1, 1, 8, 128, 0, 1, 5, 0, None, None)
+    assert rc == _lib.TC_ERR_INVALID_ARGUMENT  # one kept row needs its pointers
     rc = lib.tc_shift_keys(4096, st, 4096, st, 1, 8, 10, 128, 0, table, None)
     assert rc == _lib.TC_ERR_INVALID_ARGUMENT and b"alias" in lib.tc_last_error()
     assert lib.tc_shift_keys(4096, st, 8192, st, 1, 8, 0, 128, 0, table, None) == _lib.TC_OK

@@ -124,6 +124,21 @@ def test_copy_splice_matches_oracle(gpu):
         assert np.array_equal(bits(layer.values), bits(rv))
 
 
+@pytest.mark.parametrize("s", [Split(0, 5, 0), Split(0, 0, 0), Split(0, 300, 0)])
+def test_copy_splice_keeping_nothing(gpu, s):
+    """A split that keeps no token empties a plain DynamicLayer cache, as the reference's
+    index_select does (threadcut/kv.py:34-41); appends continue from position 0."""
+    ks, vs = workloads.layer_caches(24, 2, 300)
+    cache = DynamicCache(config=Qwen3Config(num_hidden_layers=2))
+    for layer, k, v in zip(cache.layers, ks, vs):
+        layer.update(k.to(gpu), v.to(gpu))
+    kv.splice(cache, s, workloads.inv_freq(1e6))
+    for layer, k, v in zip(cache.layers, ks, vs):
+        assert layer.keys.shape == (1, 8, 0, 128) and layer.values.shape == (1, 8, 0, 128)
+        layer.update(k[:, :, :3].to(gpu), v[:, :, :3].to(gpu))
+        assert torch.equal(layer.keys.cpu(), k[:, :, :3]) and torch.equal(layer.values.cpu(), v[:, :, :3])
+
+
 def test_shift_keys_matches_oracle_and_reference_ops(gpu):
     g = torch.Generator().manual_seed(23)
     kbuf = torch.randn(2, 8, 600, 128, generator=g).half()

@@ -514,6 +514,7 @@ int tc_splice_copy(void* const* k_src_host, void* const* v_src_host, const int64
                 (long long)c0, (long long)c);
   if (c0 + c > src_tokens || a > src_tokens)
     return fail(TC_ERR_INVALID_ARGUMENT, "split past the %lld source tokens", (long long)src_tokens);
+  if (a + c == 0) return TC_OK;  // nothing kept: the destination is empty and needs no pointers
   if ((rc = check_ptrs("k_src", k_src_host, num_layers)) != TC_OK) return rc;
   if ((rc = check_ptrs("v_src", v_src_host, num_layers)) != TC_OK) return rc;
   if ((rc = check_ptrs("k_dst", k_dst_host, num_layers)) != TC_OK) return rc;
