@@ -430,8 +430,9 @@ class PagedKV:
 
     def write_step(self, layer, k_new, v_new):
         """The unfused order of a decode step: write one layer's new K/V rows ([B, Hkv, D] or
-        [B, Hkv, 1, D]) into the slots reserve_step() took, with two torch row copies. After
-        every layer is written (here or by decode_append), decode() reads the new token."""
+        [B, Hkv, 1, D]) into the slots reserve_step() took, with two torch row copies. Once a
+        layer's row is written (here or by decode_append), decode() and prefill() of that layer
+        read the new token; prune() and the next reserve_step() wait for every layer."""
         step = getattr(self, "_step", None)
         if step is None or step[0] != self.table.version or layer not in step[1]:
             raise RuntimeError(f"PagedKV.write_step: layer {layer} has no reserved slot in this step")
