@@ -4,8 +4,9 @@
  * outputs back to raw files. tests/test_gpu_c_host.py writes the inputs and
  * checks the outputs.
  *
- *   tc_host decode DIR   meta.txt: B Hkv G N D scale split dtype
- *                        q.bin [B,Hkv,G,D], k.bin / v.bin [B,Hkv,N,D] (2-byte elements)
+ *   tc_host decode DIR   meta.txt: B Hkv G N D scale split dtype ragged
+ *                        q.bin [B,Hkv,G,D], k.bin / v.bin [B,Hkv,N,D] (2-byte elements),
+ *                        lens.bin int32 [B] (tokens of each sequence) when ragged is 1
  *                        -> out.bin (tc_decode_attention, workspace from hipMalloc)
  *                           out_noalloc.bin (tc_decode_attention_noalloc)
  *   tc_host prefill DIR  meta.txt: B Hq Hkv Q N D scale causal mask_batch dtype
@@ -86,11 +87,11 @@ static void* to_device(const void* host, size_t bytes) {
 }
 
 static int decode(const char* dir) {
-  int b, hkv, g, d, split, dtype;
+  int b, hkv, g, d, split, dtype, ragged;
   long long n;
   float scale;
   FILE* m = fopen(path_in(dir, "meta.txt"), "r");
-  if (!m || fscanf(m, "%d %d %d %lld %d %f %d %d", &b, &hkv, &g, &n, &d, &scale, &split, &dtype) != 8) {
+  if (!m || fscanf(m, "%d %d %d %lld %d %f %d %d %d", &b, &hkv, &g, &n, &d, &scale, &split, &dtype, &ragged) != 9) {
     fprintf(stderr, "tc_host: bad meta.txt\n");
     return 1;
   }
@@ -104,15 +105,18 @@ static int decode(const char* dir) {
   const int64_t qs[3] = {(int64_t)hkv * g * d, (int64_t)g * d, d};
   const int64_t ks[3] = {(int64_t)hkv * n * d, (int64_t)n * d, d};
 
+  int32_t* lens = ragged ? read_file(dir, "lens.bin", (size_t)b * sizeof(int32_t)) : NULL;
+  int32_t* lens_d = ragged ? to_device(lens, (size_t)b * sizeof(int32_t)) : NULL;
+
   /* The caller sizes the workspace with the library's own split arithmetic. */
-  const int splits = tc_decode_num_splits(b, hkv, n, split, 0);
+  const int splits = tc_decode_num_splits(b, hkv, n, split, ragged);
   if (splits < 0) abi_ok(-splits, "tc_decode_num_splits");
   const size_t ws_bytes = tc_decode_workspace_bytes(b, hkv, g, d, splits);
   void* ws = to_device(NULL, ws_bytes);
-  abi_ok(tc_decode_attention(qd, qs, kd, ks, vd, ks, NULL, n, b, hkv, g, d, dtype, scale, split, ws, ws_bytes,
+  abi_ok(tc_decode_attention(qd, qs, kd, ks, vd, ks, lens_d, n, b, hkv, g, d, dtype, scale, split, ws, ws_bytes,
                              od, qs, NULL),
          "tc_decode_attention");
-  abi_ok(tc_decode_attention_noalloc(qd, qs, kd, ks, vd, ks, NULL, n, b, hkv, g, d, dtype, scale, split, od2, qs,
+  abi_ok(tc_decode_attention_noalloc(qd, qs, kd, ks, vd, ks, lens_d, n, b, hkv, g, d, dtype, scale, split, od2, qs,
                                      NULL),
          "tc_decode_attention_noalloc");
   hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -124,6 +128,7 @@ static int decode(const char* dir) {
   write_file(dir, "out_noalloc.bin", out, q_bytes);
   printf("decode B=%d Hkv=%d G=%d N=%lld splits=%d workspace=%zu\n", b, hkv, g, n, splits, ws_bytes);
   hipFree(qd); hipFree(kd); hipFree(vd); hipFree(od); hipFree(od2); hipFree(ws);
+  if (ragged) { hipFree(lens_d); free(lens); }
   free(q); free(k); free(v); free(out);
   return 0;
 }

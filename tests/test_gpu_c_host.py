@@ -63,14 +63,18 @@ def from_bits(raw, shape, dtype):
     return torch.from_numpy(np.frombuffer(raw, dtype=np.int16).copy()).view(dtype).reshape(shape)
 
 
-def host_decode(tmp, q, k, v, scale, split, dtype):
-    """q [B, Hkv, G, D], k/v [B, Hkv, N, D] CPU tensors -> (out, out_noalloc) from the C host."""
+def host_decode(tmp, q, k, v, scale, split, dtype, lens=None):
+    """q [B, Hkv, G, D], k/v [B, Hkv, N, D] CPU tensors (lens: int32 [B] or None) -> (out,
+    out_noalloc) from the C host."""
     b, hkv, g, _ = q.shape
     n = k.shape[2]
+    if lens is not None:
+        (tmp / "lens.bin").write_bytes(lens.numpy().astype(np.int32).tobytes())
     (tmp / "q.bin").write_bytes(bits(q))
     (tmp / "k.bin").write_bytes(bits(k))
     (tmp / "v.bin").write_bytes(bits(v))
-    (tmp / "meta.txt").write_text(f"{b} {hkv} {g} {n} {D} {scale!r} {split} {DTYPE_CODE[dtype]}\n")
+    (tmp / "meta.txt").write_text(f"{b} {hkv} {g} {n} {D} {scale!r} {split} {DTYPE_CODE[dtype]} "
+                                  f"{int(lens is not None)}\n")
     run_host("decode", tmp)
     return (from_bits((tmp / "out.bin").read_bytes(), q.shape, dtype),
             from_bits((tmp / "out_noalloc.bin").read_bytes(), q.shape, dtype))
@@ -103,6 +107,25 @@ def test_c_host_decode_matches_closed_form(gpu, tmp_path, dtype, b, hkv, g, n, s
     assert (np.abs(out.float().numpy() - want) - (tol + rel * np.abs(want))).max() <= 0
     assert torch.equal(out.view(torch.int16), out_na.view(torch.int16))
     py = flash_decode.decode_attention_batched(q.to(gpu), k.to(gpu), v.to(gpu), scale, split=split or None)
+    assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_c_host_ragged_decode(gpu, tmp_path, dtype):
+    """Per-sequence lengths (tc_decode_attention's lens, empty and 1-token sequences included)."""
+    b, hkv, g, n = 6, 8, 4, 5000
+    gen = torch.Generator().manual_seed(99)
+    q = torch.randn(b, hkv, g, D, generator=gen).to(dtype)
+    k = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    v = torch.randn(b, hkv, n, D, generator=gen).to(dtype)
+    lens = torch.tensor([5000, 0, 1, 1234, 4097, 17], dtype=torch.int32)
+    scale = D ** -0.5
+    out, out_na = host_decode(tmp_path, q, k, v, scale, 0, dtype, lens)
+    want = od.decode_ragged(q.float().numpy(), k.float().numpy(), v.float().numpy(), lens.numpy(), scale)
+    tol, rel = (2e-3, 0.0) if dtype == torch.float16 else (4e-3, 2.0 ** -8)
+    assert (np.abs(out.float().numpy() - want) - (tol + rel * np.abs(want))).max() <= 0
+    assert torch.equal(out.view(torch.int16), out_na.view(torch.int16))
+    py = flash_decode.decode_attention_batched(q.to(gpu), k.to(gpu), v.to(gpu), scale, lens=lens.to(gpu))
     assert torch.equal(py.cpu().view(torch.int16), out.view(torch.int16))
 
 
