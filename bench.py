@@ -798,7 +798,7 @@ def measure_paged(dev, n, steps, page_tokens=64):
     s = workloads.SPLICE_SPLIT
     cache = filled(workloads.SPLICE_TOKENS, 7)
     suffix = _cut(cache.table.frags[0], s.c0, s.c0 + s.c)
-    tiles = tiles_of(suffix)
+    tiles = tiles_of(suffix, page_tokens)
     t = torch.zeros((len(tiles), 4), dtype=torch.int32)
     t[:, :3] = torch.from_numpy(tiles)
     td = t.to(dev)
@@ -821,7 +821,7 @@ def measure_paged(dev, n, steps, page_tokens=64):
         pt.frags = [cache.table.frags[0].copy()]
         pt.free = list(cache.table.free)
         suf, freed = pt.prune(0, s.a, s.c0, s.c)
-        tiles_of(suf)
+        tiles_of(suf, page_tokens)
     host_us = (time.perf_counter() - t0) * 1e6 / reps
     out["prune_splice_split"] = {
         "split": [s.a, s.c0, s.c], "tokens": workloads.SPLICE_TOKENS, "layers": LAYERS,

@@ -255,8 +255,11 @@ int tc_decode_paged_append_attention(const void* q_dev, const int64_t q_strides[
  * lens_dev[b] tokens before the step; its new token goes to logical position
  * lens_dev[b], whose row sits tok_off_dev[b * tok_pitch + lens_dev[b]] bytes
  * into the head slab of the pools (an offset outside the pool writes
- * nothing). The tile table covers slots reserved ahead: each entry's 4th word
- * is its first logical position, and only rows below lens_dev[b] are read.
+ * nothing). A sequence whose lens_dev[b] is tok_pitch or more has no offset
+ * row for its new token: nothing is written for it, and the call still
+ * attends its cached rows below lens_dev[b] and the new token. The tile table
+ * covers slots reserved ahead: each entry's 4th word is its first logical
+ * position, and only rows below lens_dev[b] are read.
  * The split plan depends on max_tiles only, so the caller advances lens_dev
  * between steps (on the device, inside the graph) and nothing else changes.
  * Pools must be under 2 GiB (32-bit offsets). Workspace as
@@ -436,7 +439,10 @@ int tc_match_split(const int64_t* cached, int64_t n_cached, const int64_t* fresh
  * it; threadcut/kv.py:28-41,83-92 is the move it replaces): no reference
  * function has these signatures. A sequence is a list of fragments, rows of
  * int64 {page, first slot, count} in logical order (count >= 1 consecutive
- * slots of one page).
+ * slots of one page). Each function takes the pool's page size, page_tokens,
+ * and refuses (TC_ERR_INVALID_ARGUMENT) a list with a fragment that runs past
+ * its page (first slot + count > page_tokens), a negative page or slot, or an
+ * empty fragment.
  *
  * Tile entries {page, first slot, rows, logical start} of the fragments, each
  * cut at multiples of 16 slots (the tile table of tc_decode_paged_attention,
@@ -444,7 +450,8 @@ int tc_match_split(const int64_t* cached, int64_t n_cached, const int64_t* fresh
  * logical position first_pos. Returns the number of entries and writes them
  * only when max_tiles is at least that (tiles may be NULL to ask), or
  * -TC_ERR_INVALID_ARGUMENT for a malformed fragment. */
-int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t first_pos, int32_t* tiles, int64_t max_tiles);
+int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t page_tokens, int64_t first_pos, int32_t* tiles,
+                      int64_t max_tiles);
 
 /* Prune of one sequence: keep logical tokens [0, a) and [c0, c0 + c). kept
  * (room for num_frags + 1 rows) receives the new fragment list, the two kept
@@ -452,8 +459,8 @@ int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t first_pos
  * page); suffix (num_frags rows) the fragments of [c0, c0 + c) alone; freed
  * (num_frags entries) the pages no kept fragment uses, ascending.
  * counts = {kept rows, suffix rows, freed pages}. */
-int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t a, int64_t c0, int64_t c, int64_t* kept,
-                  int64_t* suffix, int64_t* freed, int64_t counts[3]);
+int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t page_tokens, int64_t a, int64_t c0, int64_t c,
+                  int64_t* kept, int64_t* suffix, int64_t* freed, int64_t counts[3]);
 
 /* Byte offset of every logical token's row in a head slab of the pools,
  * page * page_bytes + slot * slot_bytes, for the tokens of the fragments, and
@@ -461,8 +468,8 @@ int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t a, int64_t c0
  * tc_prefill_paged_attention and tc_decode_paged_append_attention_at).
  * Returns the token count, or -TC_ERR_INVALID_ARGUMENT when it exceeds pitch,
  * a fragment is malformed or an offset passes 2^31 - 1. */
-int64_t tc_page_token_offsets(const int64_t* frags, int64_t num_frags, int64_t page_bytes, int64_t slot_bytes,
-                              int32_t* out, int64_t pitch);
+int64_t tc_page_token_offsets(const int64_t* frags, int64_t num_frags, int64_t page_tokens, int64_t page_bytes,
+                              int64_t slot_bytes, int32_t* out, int64_t pitch);
 
 #ifdef __cplusplus
 }

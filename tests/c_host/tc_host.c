@@ -187,11 +187,12 @@ static int prefill(const char* dir) {
   return 0;
 }
 
-static void* upload_tiles(const int64_t* frags, int64_t nf, int64_t* count) {
-  const int64_t nt = tc_page_tiles(frags, nf, 0, NULL, 0);
+static void* upload_tiles(const int64_t* frags, int64_t nf, int64_t page_tokens, int64_t* count) {
+  const int64_t nt = tc_page_tiles(frags, nf, page_tokens, 0, NULL, 0);
   if (nt < 0) abi_ok((int)-nt, "tc_page_tiles");
   int32_t* tiles = calloc((size_t)(nt ? nt : 1) * 4, sizeof(int32_t));
-  if (nt && tc_page_tiles(frags, nf, 0, tiles, nt) != nt) abi_ok(TC_ERR_INVALID_ARGUMENT, "tc_page_tiles");
+  if (nt && tc_page_tiles(frags, nf, page_tokens, 0, tiles, nt) != nt)
+    abi_ok(TC_ERR_INVALID_ARGUMENT, "tc_page_tiles");
   void* d = to_device(tiles, (size_t)(nt ? nt : 1) * 4 * sizeof(int32_t));
   free(tiles);
   *count = nt;
@@ -241,9 +242,9 @@ static int paged(const char* dir) {
     int64_t* suffix = malloc((size_t)nf * 3 * sizeof(int64_t));
     int64_t* freed = malloc((size_t)nf * sizeof(int64_t));
     int64_t counts[3];
-    abi_ok(tc_page_prune(frags, nf, a, c0, c, kept, suffix, freed, counts), "tc_page_prune");
+    abi_ok(tc_page_prune(frags, nf, pt, a, c0, c, kept, suffix, freed, counts), "tc_page_prune");
     int64_t nt = 0;
-    void* sd = upload_tiles(suffix, counts[1], &nt);
+    void* sd = upload_tiles(suffix, counts[1], pt, &nt);
     float* table = read_file(dir, "table.bin", (size_t)d * sizeof(float));
     void* pools[1] = {kd};
     abi_ok(tc_paged_rotate_keys(pools, 1, ps, pages, pt, sd, nt, hkv, d, dtype, table, NULL),
@@ -259,7 +260,7 @@ static int paged(const char* dir) {
   }
 
   int64_t mt = 0;
-  void* tab = upload_tiles(frags, nf, &mt);
+  void* tab = upload_tiles(frags, nf, pt, &mt);
   const int32_t cnt = (int32_t)mt;
   void* cnt_d = to_device(&cnt, sizeof cnt);
   if (mt < 1) mt = 1;  /* the table's width, as the library sizes it */

@@ -51,7 +51,7 @@ def test_noalloc_refuses_plans_beyond_its_scratch(lib):
 
 
 def test_version_and_messages(lib):
-    assert lib.tc_abi_version() == 1
+    assert lib.tc_abi_version() == 2
     for code in range(6):
         assert lib.tc_strerror(code)
     assert lib.tc_strerror(99) == b"unknown error"

@@ -242,6 +242,31 @@ def test_fused_paged_append_matches_append_then_decode(gpu, lens, P, dt):
         fused.decode_append(0, qs[0].to(gpu), kn[0].to(gpu), vn[0].to(gpu), SCALE)
 
 
+@pytest.mark.parametrize("past", [0, 5])
+def test_device_length_step_past_the_offset_rows_writes_nothing(gpu, past):
+    """tc_decode_paged_append_attention_at with lens[b] at or past the offset table's rows
+    (no slot holds position lens[b]): the pools stay unchanged, and the output is attention
+    over the cached rows below lens[b] that the table holds plus the new token."""
+    n, P = 100, 16
+    cache, host = filled(gpu, 1, [n], P, seed=71)
+    off, pitch = cache.device_offsets()
+    assert pitch == n
+    gen = torch.Generator().manual_seed(72)
+    q = torch.randn(1, 8, 4, 128, generator=gen).half()
+    kn = torch.randn(1, 8, 128, generator=gen).half()
+    vn = torch.randn(1, 8, 128, generator=gen).half()
+    before = (cache.k_pools[0].clone(), cache.v_pools[0].clone())
+    lens = torch.tensor([n + past], dtype=torch.int32, device=gpu)
+    print(f"case: device-length step at lens={n + past}, pitch={pitch}", flush=True)
+    out = cache.decode_append_at(0, q.to(gpu), kn.to(gpu), vn.to(gpu), lens, SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k_pools[0], before[0]) and torch.equal(cache.v_pools[0], before[1])
+    k = torch.cat([host[0][0][0], kn[0].unsqueeze(1)], dim=1)
+    v = torch.cat([host[0][0][1], vn[0].unsqueeze(1)], dim=1)
+    want = closed_form(q[0], k, v)
+    assert np.abs(out[0].float().cpu().numpy() - want).max() <= TOL[torch.float16]
+
+
 def test_decode_and_prune_refused_while_a_step_is_pending(gpu):
     """After reserve_step() the tile table holds each sequence's unwritten slot: decode() of a
     layer refuses until that layer has run decode_append, prune() until every layer has (or

@@ -170,6 +170,33 @@ def test_paged_cache_matches_growing_cache(model):
 
 
 @torch.no_grad()
+def test_dropped_paged_caches_free_their_pools(model):
+    """A server makes a fresh cache whenever a turn cannot be spliced (threadcut/engine.py:55):
+    paged caches that nothing holds any more give their pools back (the layer registry holds
+    its entries weakly), so device memory returns to where it started."""
+    import gc
+
+    ids = ids_of(150, 23)
+
+    def turn(i):
+        pc = paged.new_paged_cache(model.config, num_pages=64, page_tokens=16)
+        run(model, ids[:120], pc)
+        run(model, [ids[120 + i]], pc)
+        assert paged.state_of(pc).kv is not None
+
+    turn(0)  # warm-up: whatever the forward allocates once
+    gc.collect()
+    torch.cuda.synchronize()
+    start, registered = torch.cuda.memory_allocated(), len(paged._LAYERS)
+    for i in range(1, 5):
+        turn(i)
+    gc.collect()
+    torch.cuda.synchronize()
+    assert len(paged._LAYERS) == registered
+    assert torch.cuda.memory_allocated() == start
+
+
+@torch.no_grad()
 def test_paged_splice_matches_fresh_compute(model):
     """T2 on the paged cache: A·B·C (each span computed alone) pruned to A·C by kv.splice (pages
     of B freed, C's keys re-rotated in place), then D and two decode steps, against a fresh

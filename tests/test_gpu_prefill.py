@@ -230,8 +230,14 @@ def test_strided_cache_views_and_scales(gpu):
     check(q * 4, k, v, causal=True, scale=1.0, label="large scores")
 
 
-def test_through_attention_interface(gpu):
-    """attention.attention() takes the kernel for both prefill masks the model produces."""
+def test_through_attention_interface(gpu, monkeypatch):
+    """attention.attention() takes the kernel for both prefill masks the model produces: the
+    reference's route (repeat_kv + SDPA, attention.py:43-46) raises if it is reached."""
+    def no_sdpa(*args, **kwargs):
+        raise AssertionError("a supported prefill call reached SDPA instead of the HIP kernel")
+
+    monkeypatch.setattr(attention.F, "scaled_dot_product_attention", no_sdpa)
+    monkeypatch.setattr(attention, "repeat_kv", no_sdpa)
     q, k, v = workloads.prefill_inputs(12, q_len=96, n=96, device=gpu)
     out, w = attention.attention(None, q, k, v, None, scaling=SCALE)
     assert w is None

@@ -83,7 +83,12 @@ class _Cache:
 
 
 @pytest.mark.parametrize("seed", range(80))
-def test_random_splice(gpu, seed):
+def test_random_splice(gpu, seed, monkeypatch):
+    def no_torch(*args, **kwargs):
+        raise AssertionError("a GPU splice reached the torch op sequence instead of the HIP kernel")
+
+    for name in ("_splice_layer_torch", "_shift_keys_torch", "_splice_index_select_torch"):
+        monkeypatch.setattr(kv, name, no_torch)
     r = random.Random(seed)
     layers, batch, heads = r.randint(1, 3), r.choice([1, 1, 2]), r.choice([1, 2, 8])
     n = r.randint(2, 6000)

@@ -16,6 +16,18 @@ from threadcut_amd.match import Split
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def kernels_only(monkeypatch):
+    """Every splice here runs on GPU buffers, so it must take the HIP kernels: the reference's
+    torch op sequences (what host buffers run) raise if anything routes to them. The torch
+    ops give the oracle's bits too, so without this guard a routing mistake would pass."""
+    def no_torch(*args, **kwargs):
+        raise AssertionError("a GPU splice reached the torch op sequence instead of the HIP kernel")
+
+    for name in ("_splice_layer_torch", "_shift_keys_torch", "_splice_index_select_torch"):
+        monkeypatch.setattr(kv, name, no_torch)
+
+
 def bits(t):
     if isinstance(t, torch.Tensor):
         t = t.detach().cpu()

@@ -67,9 +67,9 @@ def test_tiles_match_restatement():
         P = rnd.choice([16, 48, 64, 100])
         frags = random_frags(rnd, P, rnd.randint(0, 30), 200)
         first = rnd.randint(0, 1000)
-        got = _tiles(np.array(frags, dtype=np.int64).reshape(-1, 3), first)
+        got = _tiles(np.array(frags, dtype=np.int64).reshape(-1, 3), P, first)
         assert np.array_equal(got, tiles_ref(frags, first)), (trial, frags)
-        assert np.array_equal(tiles_of(np.array(frags, dtype=np.int64).reshape(-1, 3)), tiles_ref(frags)[:, :3])
+        assert np.array_equal(tiles_of(np.array(frags, dtype=np.int64).reshape(-1, 3), P), tiles_ref(frags)[:, :3])
 
 
 def test_prune_matches_restatement():
@@ -138,9 +138,31 @@ def test_token_offsets_refuse_2gib():
 def test_malformed_fragments_are_refused():
     lib = _lib.load()
     bad = np.array([[0, 5, 0]], dtype=np.int64)  # empty fragment
-    assert lib.tc_page_tiles(bad.ctypes.data, 1, 0, None, 0) == -_lib.TC_ERR_INVALID_ARGUMENT
+    assert lib.tc_page_tiles(bad.ctypes.data, 1, 64, 0, None, 0) == -_lib.TC_ERR_INVALID_ARGUMENT
     neg = np.array([[-1, 0, 4]], dtype=np.int64)
-    assert lib.tc_page_tiles(neg.ctypes.data, 1, 0, None, 0) == -_lib.TC_ERR_INVALID_ARGUMENT
+    assert lib.tc_page_tiles(neg.ctypes.data, 1, 64, 0, None, 0) == -_lib.TC_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("frag", [[0, 60, 5], [0, 0, 65], [2, 64, 1], [1, -1, 3], [1, 3, 0]])
+def test_fragments_past_their_page_are_refused(frag):
+    """A fragment whose slots run past its page (first slot + count > page_tokens) would
+    name rows of the next page or head: every page-table entry point refuses it."""
+    lib = _lib.load()
+    f = np.array([[3, 0, 16], frag], dtype=np.int64)
+    INVALID = _lib.TC_ERR_INVALID_ARGUMENT
+    assert lib.tc_page_tiles(f.ctypes.data, 2, 64, 0, None, 0) == -INVALID
+    out = np.zeros(200, dtype=np.int32)
+    assert lib.tc_page_token_offsets(f.ctypes.data, 2, 64, 64 * 256, 256, out.ctypes.data, 200) == -INVALID
+    buf = np.zeros(64, dtype=np.int64)
+    counts = np.zeros(3, dtype=np.int64)
+    rc = lib.tc_page_prune(f.ctypes.data, 2, 64, 0, 0, 1, buf.ctypes.data, buf[20:].ctypes.data,
+                           buf[40:].ctypes.data, counts.ctypes.data_as(_lib._I64P))
+    assert rc == INVALID
+    # The same list with the fragment inside its page is taken, and page_tokens < 1 is refused.
+    ok = np.array([[3, 0, 16], [0, 48, 16]], dtype=np.int64)
+    assert lib.tc_page_tiles(ok.ctypes.data, 2, 64, 0, None, 0) == 2
+    assert lib.tc_page_tiles(ok.ctypes.data, 2, 0, 0, None, 0) == -INVALID
+    assert lib.tc_page_tiles(ok.ctypes.data, 2, 63, 0, None, 0) == -INVALID
     pt = PageTable(4, 64)
     pt.frags = [np.array([[0, 0, 10]], dtype=np.int64)]
     with pytest.raises(ValueError):

@@ -25,7 +25,7 @@ def check_table(t, model):
     assert len(t.free) == len(set(t.free))
     tab, cnt = t.tile_table()
     for b in range(t.batch):
-        ts = tiles_of(t.frags[b]).tolist()
+        ts = tiles_of(t.frags[b], t.page_tokens).tolist()
         assert cnt[b] == len(ts)
         rows = []
         for (page, slot, n), e in zip(ts, tab[b].tolist()):

@@ -79,9 +79,9 @@ SIGNATURES = {
     "tc_prefill_tiles_bytes": (_S, [_I64, _I64, _I, _I, _I]),
     "tc_prefill_mask_tiles": (_I, [_P, _I64P, _I, _I64, _I64, _I, _I, _P, _S, _P]),
     "tc_match_split": (_I, [_I64P, _I64, _I64P, _I64, _I64, _I, _I64P]),
-    "tc_page_tiles": (_I64, [_P, _I64, _I64, _P, _I64]),
-    "tc_page_prune": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64P]),
-    "tc_page_token_offsets": (_I64, [_P, _I64, _I64, _I64, _P, _I64]),
+    "tc_page_tiles": (_I64, [_P, _I64, _I64, _I64, _P, _I64]),
+    "tc_page_prune": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64P]),
+    "tc_page_token_offsets": (_I64, [_P, _I64, _I64, _I64, _I64, _P, _I64]),
 }
 
 _lock = threading.Lock()

@@ -67,6 +67,6 @@ const char* tc_strerror(int code) {
 
 const char* tc_last_error(void) { return tc::g_last_error; }
 
-int tc_abi_version(void) { return 1; }
+int tc_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -60,10 +60,23 @@ namespace {
 #ifndef TC_DECODE_WGS_PER_CU
 #define TC_DECODE_WGS_PER_CU 1  // partial work-groups per compute unit the split heuristic aims at
 #endif
+#ifndef TC_DECODE_VT
+#define TC_DECODE_VT 1  // V staging: 0 transposed in registers (v_perm), 1 row-major + transposing LDS reads
+#endif
+#ifndef TC_DECODE_LOOP
+#define TC_DECODE_LOOP 1  // tile loop: 1 loads only the tiles a wave owns
+#endif
+#ifndef TC_DECODE_WPE
+#define TC_DECODE_WPE 1  // amdgpu_waves_per_eu floor of the partial kernel (2 caps a wave at 256 registers)
+#endif
+#ifndef TC_COMBINE_ROUND
+#define TC_COMBINE_ROUND 16  // splits per lane and round of the combine
+#endif
 
 constexpr int kHeadDim = 128;
 constexpr int64_t kMaxTokens = int64_t(1) << 29;  // token positions stay 32-bit in the kernel
 constexpr int kWaves = TC_DECODE_WAVES;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kDepth = TC_DECODE_DEPTH;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
 constexpr int kSplitGranule = kWaves * kWaveIter > 64 ? kWaves * kWaveIter : 64;  // split length granule
@@ -243,15 +256,23 @@ template <> struct DecodeMma<TC_DTYPE_BF16> {
 // dims) then hit distinct banks in each half-wave.
 __host__ __device__ constexpr int vt_word(int d) { return 8 * d + 4 * (d >> 3); }
 constexpr int kVtWords = vt_word(kHeadDim);   // per wave
+// Row-major V tile in a wave's LDS region: 16 token rows of 256 bytes, each
+// padded to 288 so that the transposing reads (4 rows x 32 bytes per 16-lane
+// group, 16 rows per instruction) and the 16-byte row stores fall on distinct
+// banks.
+constexpr int kVRowBytes = 2 * kHeadDim + 32;
+constexpr int kVTileWords = 16 * kVRowBytes / 4;
+constexpr int kVStageWords = TC_DECODE_VT ? kVTileWords : kVtWords;
+typedef short lds_s4 __attribute__((ext_vector_type(4)));
 constexpr float kLazyMax = 8.f;               // log2 units the running maximum may lag
 
 // APPEND: the kernel attends (and writes) the new token of an append call
 // (a.k_new != null); the other instantiation carries none of that code.
 template <int DT, bool PAGED, bool APPEND>
-__global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const PartialArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TC_DECODE_WPE))) void decode_partial_kernel(const PartialArgs a) {
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
-  __shared__ uint32_t s_vt[kWaves][kVtWords];
+  __shared__ uint32_t s_vt[kWaves][kVStageWords];
   __shared__ float s_acc[kWaves][8][kHeadDim];
   __shared__ float s_m[kWaves][8];
   __shared__ float s_l[kWaves][8];
@@ -283,8 +304,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     const int32_t ntiles = min(max(a.tiles[b], 0), static_cast<int32_t>(a.max_tiles));
     len = 16 * ntiles;
     tab = a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4;
-    if (a.tok_off)
-      plen = min(max(a.lens[b], 0), static_cast<int32_t>(a.tok_pitch) - 1);
+    if (a.tok_off) plen = max(a.lens[b], 0);
     else if (APPEND)
       last_tile = ntiles - 1;
   } else if (a.lens) {
@@ -373,7 +393,14 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     mfma_f4 s1 = M::qk(tl.k[1], qb[1], mfma_f4{0.f, 0.f, 0.f, 0.f});
     s0 = M::qk(tl.k[2], qb[2], s0);
     s1 = M::qk(tl.k[3], qb[3], s1);
-    // V^T rows into LDS while the matrix core works.
+    // V into LDS while the matrix core works.
+#if TC_DECODE_VT
+    // Row-major: lane (g, n) stores tokens 4g + j, dims 8n .. 8n + 7.
+    char* vrow = reinterpret_cast<char*>(vt);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(vrow + (4 * g + j) * kVRowBytes + 16 * n) = tl.v[j];
+#else
+    // V^T rows, transposed in registers.
     const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&tl.v[0]);
     const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&tl.v[1]);
     const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&tl.v[2]);
@@ -385,6 +412,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       const uint32_t x23 = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);
       *reinterpret_cast<uint2*>(vt + vt_word(8 * n + e) + 2 * g) = make_uint2(x01, x23);
     }
+#endif
     float x[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -411,12 +439,36 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
     const uint2 phi = make_uint2(h01, h23), plo = make_uint2(r01, r23);
 #pragma unroll
     for (int bm = 0; bm < 8; ++bm) {
+#if TC_DECODE_VT
+      // A operand V^T[16 bm + n][4g .. 4g + 3]: ds_read_b64_tr_b16 hands lane n
+      // of a 16-lane group element (n % 4) of what lane 4 j + n / 4 addressed,
+      // for j = 0..3; lane (g, n) addresses row 4g + n / 4, dims 16 bm + 4 (n % 4).
+      const lds_s4 t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) lds_s4*)(vrow + (4 * g + (n >> 2)) * kVRowBytes + 32 * bm + 8 * (n & 3)));
+      const uint2 av = __builtin_bit_cast(uint2, t4);
+#else
       const uint2 av = *reinterpret_cast<const uint2*>(vt + vt_word(16 * bm + n) + 2 * g);
+#endif
       acc[bm] = M::pv(av, phi, acc[bm]);
       acc[bm] = M::pv(av, plo, acc[bm]);
     }
   };
 
+#if TC_DECODE_LOOP
+  // Two tiles in flight: the next tile's loads are issued before the current
+  // tile is consumed, and no load is issued past the wave's last tile.
+  if (tok < end) {
+    for (;;) {
+      const int32_t tok1 = tok + tok_step, tok2 = tok1 + tok_step;
+      load(t[1], tok1);
+      step(t[0], tok, PAGED ? tok + t[0].rows : end);
+      load(t[0], tok2);
+      if (tok1 < end) step(t[1], tok1, PAGED ? tok1 + t[1].rows : end);
+      tok = tok2;
+      if (tok >= end) break;
+    }
+  }
+#else
   if (tok < end) {
     for (;;) {
       bool done = false;
@@ -432,6 +484,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       if (done) break;
     }
   }
+#endif
 
   if (APPEND && split == 0 && wave == 0) {
     // The appended token as a tile whose only row is token 0 (the buffer
@@ -454,11 +507,11 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
       uint16_t* dst = nullptr;
       if constexpr (PAGED) {
         // The new token's slot: with device lengths, the offset table's row of
-        // position lens[b] (an offset outside the pool writes nothing);
-        // otherwise the last row of the sequence's last tile (an invalid entry,
-        // or no tile, writes nothing).
+        // position lens[b] (a position past the table's rows, or an offset
+        // outside the pool, writes nothing); otherwise the last row of the
+        // sequence's last tile (an invalid entry, or no tile, writes nothing).
         if (plen >= 0) {
-          const int32_t off = a.tok_off[static_cast<int64_t>(b) * a.tok_pitch + plen];
+          const int32_t off = plen < a.tok_pitch ? a.tok_off[static_cast<int64_t>(b) * a.tok_pitch + plen] : -1;
           const int64_t room = static_cast<int64_t>(a.pages) * a.sk_b * 2 - h * a.sk_h * 2 - kHeadDim * 2;
           if (off >= 0 && off <= room) {
             char* base = reinterpret_cast<char*>(is_v ? a.v_w + h * a.sv_h : a.k_w + h * a.sk_h);
@@ -481,6 +534,21 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
 
   // The head's sum over the four lane groups; m is already common to them.
   l = rows_sum(l);
+  const int64_t part = (static_cast<int64_t>(b) * a.heads + h) * a.splits + split;
+  if constexpr (kWaves == 1) {
+    // One wave: its accumulator is the split's; lane (g, n) holds dims
+    // 16 bm + 4 g .. + 3 of head n.
+    if (n < a.group) {
+      const float inv = l == 0.f ? 0.f : __builtin_amdgcn_rcpf(l);
+      float* o = a.o_part + (part * a.group + n) * kHeadDim + 4 * g;
+#pragma unroll
+      for (int bm = 0; bm < 8; ++bm)
+        *reinterpret_cast<float4*>(o + 16 * bm) =
+            make_float4(acc[bm][0] * inv, acc[bm][1] * inv, acc[bm][2] * inv, acc[bm][3] * inv);
+      if (g == 0) a.lse_part[part * a.group + n] = (l == 0.f) ? neg_inf() : (m + __builtin_amdgcn_logf(l)) * kLn2;
+    }
+    return;
+  }
   if (n < a.group) {
 #pragma unroll
     for (int bm = 0; bm < 8; ++bm)
@@ -491,8 +559,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
   __syncthreads();
 
   // Each thread merges two adjacent dims of one head (one pass for G <= 4).
-  const int64_t part = (static_cast<int64_t>(b) * a.heads + h) * a.splits + split;
-  for (int idx = threadIdx.x; idx < a.group * (kHeadDim / 2); idx += 64 * kWaves) {
+  for (int idx = threadIdx.x; idx < a.group * (kHeadDim / 2); idx += kThreads) {
     const int hh = idx / (kHeadDim / 2);
     const int d = 2 * (idx % (kHeadDim / 2));
     float mw[kWaves], lw[kWaves];
@@ -530,7 +597,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_partial_kernel(const Parti
 // round covers up to 2 * kCombineRound splits). Each round folds its splits
 // into a running (max, sum, weighted o) with one exponential per split; one
 // permlane32 swap merges the two halves.
-constexpr int kCombineRound = 16;   // splits per lane and round
+constexpr int kCombineRound = TC_COMBINE_ROUND;   // splits per lane and round
 
 // x of the lane pair (l, l ^ 16) or (l, l ^ 32): the lower row's value in lo,
 // the upper row's in hi, in both lanes.
@@ -653,10 +720,10 @@ inline dim3 partial_grid(const PartialArgs& a, int batch) { return dim3(a.heads,
 template <int DT, bool PAGED>
 void launch_partial_paged(const PartialArgs& a, int batch, hipStream_t stream) {
   if (a.k_new)
-    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, true>), partial_grid(a, batch), dim3(64 * kWaves), 0,
+    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, true>), partial_grid(a, batch), dim3(kThreads), 0,
                        stream, a);
   else
-    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, false>), partial_grid(a, batch), dim3(64 * kWaves), 0,
+    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, false>), partial_grid(a, batch), dim3(kThreads), 0,
                        stream, a);
 }
 

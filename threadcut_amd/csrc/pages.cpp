@@ -19,11 +19,13 @@ namespace {
 
 constexpr int64_t kTile = 16;  // rows per tile (the decode kernel's wave tile)
 
-bool malformed(const int64_t* frags, int64_t num_frags) {
-  if (num_frags < 0 || (num_frags > 0 && !frags)) return true;
+// A fragment list is well formed when every fragment names a page id that
+// fits 32 bits and count >= 1 slots that stay inside one page of page_tokens.
+bool malformed(const int64_t* frags, int64_t num_frags, int64_t page_tokens) {
+  if (num_frags < 0 || (num_frags > 0 && !frags) || page_tokens < 1 || page_tokens > INT32_MAX) return true;
   for (int64_t i = 0; i < num_frags; ++i) {
     const int64_t* f = frags + 3 * i;
-    if (f[0] < 0 || f[0] > INT32_MAX || f[1] < 0 || f[2] < 1 || f[1] + f[2] > INT32_MAX) return true;
+    if (f[0] < 0 || f[0] > INT32_MAX || f[1] < 0 || f[2] < 1 || f[1] > page_tokens - f[2]) return true;
   }
   return false;
 }
@@ -56,8 +58,9 @@ std::vector<int64_t> pages_of(const int64_t* frags, int64_t num_frags) {
 
 extern "C" {
 
-int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t first_pos, int32_t* tiles, int64_t max_tiles) {
-  if (malformed(frags, num_frags) || first_pos < 0 || max_tiles < 0) return -TC_ERR_INVALID_ARGUMENT;
+int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t page_tokens, int64_t first_pos, int32_t* tiles,
+                      int64_t max_tiles) {
+  if (malformed(frags, num_frags, page_tokens) || first_pos < 0 || max_tiles < 0) return -TC_ERR_INVALID_ARGUMENT;
   int64_t n = 0;
   for (int64_t i = 0; i < num_frags; ++i) {
     const int64_t s = frags[3 * i + 1], e = s + frags[3 * i + 2];
@@ -81,9 +84,9 @@ int64_t tc_page_tiles(const int64_t* frags, int64_t num_frags, int64_t first_pos
   return n;
 }
 
-int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t a, int64_t c0, int64_t c, int64_t* kept,
-                  int64_t* suffix, int64_t* freed, int64_t counts[3]) {
-  if (malformed(frags, num_frags) || !kept || !suffix || !freed || !counts) return TC_ERR_INVALID_ARGUMENT;
+int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t page_tokens, int64_t a, int64_t c0, int64_t c,
+                  int64_t* kept, int64_t* suffix, int64_t* freed, int64_t counts[3]) {
+  if (malformed(frags, num_frags, page_tokens) || !kept || !suffix || !freed || !counts) return TC_ERR_INVALID_ARGUMENT;
   int64_t n = 0;
   for (int64_t i = 0; i < num_frags; ++i) n += frags[3 * i + 2];
   if (a < 0 || c < 0 || c0 < a || c0 + c > n) return TC_ERR_INVALID_ARGUMENT;
@@ -111,9 +114,10 @@ int tc_page_prune(const int64_t* frags, int64_t num_frags, int64_t a, int64_t c0
   return TC_OK;
 }
 
-int64_t tc_page_token_offsets(const int64_t* frags, int64_t num_frags, int64_t page_bytes, int64_t slot_bytes,
-                              int32_t* out, int64_t pitch) {
-  if (malformed(frags, num_frags) || page_bytes < 0 || slot_bytes < 0 || pitch < 0 || (pitch > 0 && !out))
+int64_t tc_page_token_offsets(const int64_t* frags, int64_t num_frags, int64_t page_tokens, int64_t page_bytes,
+                              int64_t slot_bytes, int32_t* out, int64_t pitch) {
+  if (malformed(frags, num_frags, page_tokens) || page_bytes < 0 || slot_bytes < 0 || pitch < 0 ||
+      (pitch > 0 && !out))
     return -TC_ERR_INVALID_ARGUMENT;
   int64_t t = 0;
   for (int64_t i = 0; i < num_frags; ++i) {

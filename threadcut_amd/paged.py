@@ -27,6 +27,7 @@ host code of ``tc_page_tiles``, ``tc_page_prune`` and ``tc_page_token_offsets``)
 ``PagedKV`` adds the pools.
 """
 import ctypes
+import weakref
 
 import numpy as np
 import torch
@@ -84,26 +85,27 @@ def _frag_arg(frags):
     return f, _addr(f), len(f)
 
 
-def _tiles(frags, first_pos=0):
-    """Tile entries {page, first slot, rows, logical start} of a fragment array,
-    int32 [T, 4] (tc_page_tiles): each fragment cut at multiples of 16 slots."""
+def _tiles(frags, page_tokens, first_pos=0):
+    """Tile entries {page, first slot, rows, logical start} of a fragment array of pages of
+    page_tokens slots, int32 [T, 4] (tc_page_tiles): each fragment cut at multiples of 16
+    slots."""
     lib = _lib.load()
     f, fp, nf = _frag_arg(frags)
-    n = lib.tc_page_tiles(fp, nf, int(first_pos), None, 0)
+    n = lib.tc_page_tiles(fp, nf, int(page_tokens), int(first_pos), None, 0)
     if n < 0:
         _lib.check(-n, "tc_page_tiles")
     out = np.empty((n, 4), dtype=np.int32)
     if n:
-        _lib.check(0 if lib.tc_page_tiles(fp, nf, int(first_pos), _addr(out), n) == n
+        _lib.check(0 if lib.tc_page_tiles(fp, nf, int(page_tokens), int(first_pos), _addr(out), n) == n
                    else _lib.TC_ERR_INVALID_ARGUMENT, "tc_page_tiles")
     return out
 
 
-def tiles_of(frags):
-    """Tile entries (page, first slot, rows) of a fragment array, int32 [T, 3]:
-    each fragment is cut at multiples of 16 slots, so full tiles are 16-slot
-    aligned."""
-    return np.ascontiguousarray(_tiles(frags)[:, :3])
+def tiles_of(frags, page_tokens):
+    """Tile entries (page, first slot, rows) of a fragment array of pages of page_tokens
+    slots, int32 [T, 3]: each fragment is cut at multiples of 16 slots, so full tiles are
+    16-slot aligned."""
+    return np.ascontiguousarray(_tiles(frags, page_tokens)[:, :3])
 
 
 class PageTable:
@@ -168,8 +170,9 @@ class PageTable:
         # One buffer: kept (nf + 1 rows), suffix (nf rows), freed (nf), counts (3).
         buf = np.empty(7 * nf + 6, dtype=np.int64)
         base = _addr(buf)
-        rc = _lib.load().tc_page_prune(fp, nf, int(a), int(c0), int(c), base, base + 8 * (3 * nf + 3),
-                                       base + 8 * (6 * nf + 3), ctypes.cast(base + 8 * (7 * nf + 3), _I64P))
+        rc = _lib.load().tc_page_prune(fp, nf, self.page_tokens, int(a), int(c0), int(c), base,
+                                       base + 8 * (3 * nf + 3), base + 8 * (6 * nf + 3),
+                                       ctypes.cast(base + 8 * (7 * nf + 3), _I64P))
         _lib.check(rc, "tc_page_prune")
         nk, ns, nfr = (int(x) for x in buf[7 * nf + 3:])
         self.frags[b] = buf[:3 * nk].reshape(nk, 3).copy()
@@ -196,7 +199,7 @@ class PageTable:
     def tile_table(self):
         """int32 [B, max_tiles, 4] and tiles int32 [B] (numpy): entries {page, first slot,
         rows, first logical position} in logical order."""
-        per = [_tiles(f) for f in self.frags]
+        per = [_tiles(f, self.page_tokens) for f in self.frags]
         mt = max(1, max(len(t) for t in per))
         tab = np.zeros((self.batch, mt, 4), dtype=np.int32)
         cnt = np.zeros(self.batch, dtype=np.int32)
@@ -215,7 +218,8 @@ class PageTable:
         lib = _lib.load()
         for b in range(self.batch):
             f, fp, nf = _frag_arg(self.frags[b])
-            if lib.tc_page_token_offsets(fp, nf, int(page_bytes), int(slot_bytes), _addr(off[b]), pitch) < 0:
+            if lib.tc_page_token_offsets(fp, nf, self.page_tokens, int(page_bytes), int(slot_bytes), _addr(off[b]),
+                                         pitch) < 0:
                 raise RuntimeError("PageTable.token_offsets: pools of 2 GiB or more need 64-bit offsets")
         return off
 
@@ -530,7 +534,7 @@ class PagedKV:
         self._refuse_during_step("prune")
         suffix, freed = self.table.prune(b, s.a, s.c0, s.c)
         gap = s.c0 - s.a
-        tiles = tiles_of(suffix)
+        tiles = tiles_of(suffix, self.table.page_tokens)
         if gap and len(tiles):
             t = np.zeros((len(tiles), 4), dtype=np.int32)
             t[:, :3] = tiles
@@ -552,8 +556,10 @@ class PagedKV:
 # ---------------------------------------------------------------------------
 
 # PagedLayers by the address of their K pool: update() returns the pools, and
-# the "threadcut" attention finds the layer behind them here.
-_LAYERS = {}
+# the "threadcut" attention finds the layer behind them here. The entries are
+# weak: a cache that nothing else holds is freed with its pools, and its
+# entries leave the registry with it.
+_LAYERS = weakref.WeakValueDictionary()
 
 
 def layer_of(key):
@@ -651,12 +657,17 @@ class PagedLayer(DynamicLayer):
         self.n = 0
 
     def flush(self):
-        """Write a pending row that no attention call consumed."""
+        """Write a pending row that no attention call consumed. In a captured step (device
+        lengths) only the decode kernel can place the row, at lens[b]; a row left pending
+        there would be lost, so that raises."""
         if self.pending is not None:
             k, v = self.pending
             self.pending = None
-            if self.owner.device_lens is None:
-                self.kv.write_step(self.index, k, v)
+            if self.owner.device_lens is not None:
+                raise RuntimeError(
+                    "paged cache: a one-token update of a captured decode step reached no decode attention "
+                    "call (an attention mask, or a second update before attention); its K/V row would be lost")
+            self.kv.write_step(self.index, k, v)
 
     def update(self, key_states, value_states, *args, **kwargs):
         if not self.is_initialized:
