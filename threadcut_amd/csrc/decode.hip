@@ -69,6 +69,9 @@ namespace {
 #ifndef TC_DECODE_WPE
 #define TC_DECODE_WPE 1  // amdgpu_waves_per_eu floor of the partial kernel (2 caps a wave at 256 registers)
 #endif
+#ifndef TC_DECODE_WPE_PAGED
+#define TC_DECODE_WPE_PAGED 2  // the same for the paged instantiations
+#endif
 #ifndef TC_COMBINE_ROUND
 #define TC_COMBINE_ROUND 16  // splits per lane and round of the combine
 #endif
@@ -155,6 +158,12 @@ __device__ __forceinline__ float rows_sum(float x) { return pair32_sum(pair16_su
 __device__ __forceinline__ float rows_max(float x) { return pair32_max(pair16_max(x)); }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// A wave-uniform read of memory that no kernel writes while this one runs:
+// through the constant address space it becomes a scalar load.
+__device__ __forceinline__ int32_t const_load(const int32_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(reinterpret_cast<uintptr_t>(p));
+}
 
 // Buffer resource over `bytes` bytes at p; loads past the end return zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int32_t bytes) {
@@ -269,7 +278,7 @@ constexpr float kLazyMax = 8.f;               // log2 units the running maximum 
 // APPEND: the kernel attends (and writes) the new token of an append call
 // (a.k_new != null); the other instantiation carries none of that code.
 template <int DT, bool PAGED, bool APPEND>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TC_DECODE_WPE))) void decode_partial_kernel(const PartialArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED ? TC_DECODE_WPE_PAGED : TC_DECODE_WPE))) void decode_partial_kernel(const PartialArgs a) {
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
   __shared__ uint32_t s_vt[kWaves][kVStageWords];
@@ -295,32 +304,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TC_DEC
   __asm__ volatile("" ::"s"(kslab), "s"(vslab));
   const int32_t nt = static_cast<int32_t>(a.n);
   const int32_t len_cap = APPEND ? nt - 1 : nt;
+  // The wave's first tile and the distance between its tiles.
+  int32_t tok, tok_step, wave_tokens = 0;
+  if (a.interleave) {
+    tok = (split * kWaves + wave) * kWaveIter;
+    tok_step = a.splits * kWaves * kWaveIter;
+  } else {
+    wave_tokens = a.split_tokens / kWaves;
+    tok = split * a.split_tokens + wave * wave_tokens;
+    tok_step = kWaveIter;
+  }
+  const int32_t* tab = PAGED ? a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4 : nullptr;
+  // Paged: lane i holds the table entry of the wave's i-th tile (tiles past
+  // the 64th read theirs from memory). The entries are requested before the
+  // tile count is known, bounded by the table's row, so the two reads are in
+  // flight together.
+  int32_t e_page = 0, e_slot = 0, e_cnt = 0, e_pos = 0;
+  const int32_t ti = tok + lane * tok_step;
+  if constexpr (PAGED) {
+    if ((ti >> 4) < a.max_tiles) {
+      const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (ti >> 4));
+      e_page = e.x; e_slot = e.y; e_cnt = e.z; e_pos = e.w;
+    }
+  }
   int32_t len = len_cap;
-  const int32_t* tab = nullptr;
   int32_t last_tile = -1;  // paged append: the tile whose last row is the new token's slot
   int32_t plen = -1;  // paged append with device lengths: tokens cached before this step
   if constexpr (PAGED) {
     // Token index space of 16 per tile; a tile's own row count masks the rest.
-    const int32_t ntiles = min(max(a.tiles[b], 0), static_cast<int32_t>(a.max_tiles));
+    // The tile count and lengths are read with scalar loads (constant for the
+    // kernel's lifetime).
+    const int32_t ntiles = min(max(const_load(a.tiles + b), 0), static_cast<int32_t>(a.max_tiles));
     len = 16 * ntiles;
-    tab = a.tile_tab + static_cast<int64_t>(b) * a.max_tiles * 4;
-    if (a.tok_off) plen = max(a.lens[b], 0);
+    if (a.tok_off) plen = max(const_load(a.lens + b), 0);
     else if (APPEND)
       last_tile = ntiles - 1;
   } else if (a.lens) {
     len = min(max(a.lens[b], 0), len_cap);
   }
-  int32_t tok, tok_step, end;
-  if (a.interleave) {
-    tok = (split * kWaves + wave) * kWaveIter;
-    tok_step = a.splits * kWaves * kWaveIter;
-    end = len;
-  } else {
-    const int32_t wave_tokens = a.split_tokens / kWaves;
-    tok = split * a.split_tokens + wave * wave_tokens;
-    tok_step = kWaveIter;
-    end = min(tok + wave_tokens, len);
-  }
+  const int32_t end = a.interleave ? len : min(tok + wave_tokens, len);
 
   // K: token n of the tile, bytes [64 i + 16 g, +16) for block i.
   // V: tokens 4g + j, dims 8n .. 8n + 7.
@@ -330,16 +352,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TC_DEC
     koff[i] = n * row_k + 64 * i + 16 * g;
     voff[i] = (4 * g + i) * row_v + 16 * n;
   }
-  // Paged: lane i holds the table entry of the wave's i-th tile; tiles past
-  // the 64th read theirs from memory.
-  int32_t e_page = 0, e_slot = 0, e_rows = 0;
+  // Rows each preloaded tile contributes: none past the wave's tiles; the
+  // append's last tile less the new token's row (attended from k_new); with
+  // device lengths, the rows below lens[b].
+  int32_t e_rows = 0;
   if constexpr (PAGED) {
-    const int32_t ti = tok + lane * tok_step;
     if (ti < end) {
-      const int4 e = *reinterpret_cast<const int4*>(tab + 4 * (ti >> 4));
-      e_page = e.x; e_slot = e.y;
-      e_rows = (ti >> 4) == last_tile ? e.z - 1 : e.z;  // the new token is attended from k_new
-      if (plen >= 0) e_rows = min(e.z, max(plen - e.w, 0));
+      e_rows = (ti >> 4) == last_tile ? e_cnt - 1 : e_cnt;
+      if (plen >= 0) e_rows = min(e_cnt, max(plen - e_pos, 0));
     }
   }
   int32_t li = 0;  // the wave's tiles loaded so far
@@ -641,8 +661,10 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a)
 #pragma unroll
     for (int j = 0; j < kCombineRound; ++j) {
       const int32_t s0 = r0 + 2 * j;
-      ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, o_lane, s0 * o_split, 0);
-      ls[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, l_lane, s0 * G * 4, 0));
+      // The whole offset goes in the per-lane operand, which the buffer range
+      // checks: splits past S read zero.
+      ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, o_lane + s0 * o_split, 0, 0);
+      ls[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, l_lane + s0 * G * 4, 0, 0));
     }
     // Every load of the round is in flight before the first is consumed.
     __builtin_amdgcn_sched_barrier(0);
