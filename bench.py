@@ -604,6 +604,78 @@ QWEN3_4B_CONFIG = dict(vocab_size=151936, hidden_size=2560, intermediate_size=97
                        rope_theta=1e6, tie_word_embeddings=True)
 
 
+def measure_timeline(dev, n, steps):
+    """Per-wave timeline of the decode partial kernel at n tokens (36 layers in one graph, as the
+    headline): the measurement build libthreadcut_stamps.so has every partial wave record the
+    realtime clock (100 MHz) at its start, after its first tile's step, at its loop's end,
+    after the merge barrier and after its partial stores are issued. Times are microseconds
+    from the first wave start of the same launch; percentiles over all waves of all layers.
+    The gap is from a launch's last store issue to the next launch's first wave start: the
+    partial's drain, the combine launch and its work, and the next launch."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from threadcut_amd import _lib, build, flash_decode, workloads
+
+    lib = ctypes.CDLL(build.STAMPS_LIB)
+    for name, (res, args) in _lib.SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    lib.tc_decode_set_stamps.restype = None
+    lib.tc_decode_set_stamps.argtypes = [ctypes.c_void_p]
+    qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
+    outs = [torch.empty_like(q) for q in qs]
+    plans = [flash_decode.DecodePlan(q, k, v, D ** -0.5, o) for q, k, v, o in zip(qs, ks, vs, outs)]
+    for p in plans:
+        p.lib = lib
+    S = plans[0].splits
+    waves = 4
+    stamps = torch.zeros(LAYERS, HKV * S * waves * 8, dtype=torch.int64, device=dev)
+
+    def step(record):
+        for i, p in enumerate(plans):
+            lib.tc_decode_set_stamps(stamps[i].data_ptr() if record else None)
+            p.run()
+        lib.tc_decode_set_stamps(None)
+
+    g_plain = capture(lambda: step(False))
+    g_rec = capture(lambda: step(True))
+    ms_plain = time_graph(g_plain, steps, 20, WARM_MS)
+    ms_rec = time_graph(g_rec, steps, 20, WARM_MS)
+    stamps.zero_()
+    g_rec.replay()
+    torch.cuda.synchronize()
+    raw = stamps.view(LAYERS, HKV, S, waves, 8).cpu().numpy()
+    t = raw[..., :5].astype(np.float64) * 0.01  # 100 MHz ticks -> us
+    first = t[..., 0].reshape(LAYERS, -1).min(axis=1)
+    rel = t - first[:, None, None, None, None]
+    names = ["start", "first_step_done", "loop_end", "after_barrier", "stores_issued"]
+
+    def pct(x):
+        x = x.ravel()
+        return {"p10": round(float(np.percentile(x, 10)), 3), "median": round(float(np.median(x)), 3),
+                "p90": round(float(np.percentile(x, 90)), 3), "max": round(float(x.max()), 3)}
+
+    last = t[..., 4].reshape(LAYERS, -1).max(axis=1)
+    xcc = (raw[..., 6] & 15).astype(int)
+    return {
+        "kv_tokens": n, "splits": S, "layers": LAYERS,
+        "us_per_call": round(ms_plain * 1e3 / LAYERS, 3),
+        "us_per_call_recording": round(ms_rec * 1e3 / LAYERS, 3),
+        "events_us_from_launch_start": {nm: pct(rel[..., k]) for k, nm in enumerate(names)},
+        "per_wave_us": {"start_to_first_step_done": pct(rel[..., 1] - rel[..., 0]),
+                        "loop_end_to_barrier": pct(rel[..., 3] - rel[..., 2]),
+                        "barrier_to_stores_issued": pct(rel[..., 4] - rel[..., 3])},
+        "launch_span_us_median": round(float(np.median(last - first)), 3),
+        "gap_to_next_launch_us_median": round(float(np.median(first[1:] - last[:-1])), 3),
+        "loop_end_median_by_kv_head": [round(float(np.median(rel[:, h, :, :, 2])), 3) for h in range(HKV)],
+        "xcd_of_kv_head": [int(np.bincount(xcc[:, h].ravel()).argmax()) for h in range(HKV)],
+    }
+
+
 def measure_decode_step(dev, n=10240, steps=40):
     """Whole-model decode step at the Qwen3-4B shape (random fp16 weights, 36 layers) at n
     cached tokens: the reference's eager per-token loop (engine.py:88-95) with the "threadcut"
@@ -913,7 +985,7 @@ def main():
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
     ap.add_argument("--only", choices=["decode", "partial", "yardstick", "splice", "copy", "prefill", "decode-step",
-                                       "paged"],
+                                       "paged", "decode-timeline"],
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -944,6 +1016,10 @@ def main():
         return
     if args.only == "paged":
         print(json.dumps(measure_paged(dev, args.n, max(20, args.steps // 4))))
+        return
+    if args.only == "decode-timeline":
+        print(json.dumps({str(m): measure_timeline(dev, m, args.steps) for m in
+                          ([args.n] if args.n != 10240 else [1536, 10240])}))
         return
     if args.only == "decode-step":
         print(json.dumps(measure_decode_step(dev, args.n)))

@@ -4,7 +4,10 @@ Compiles every ``csrc/*.hip`` source with hipcc (and the host-only
 ``csrc/*.cpp`` with g++) into ``_build/*.o`` in parallel, and links
 ``libthreadcut_hip.so`` next to this file, where
 ``threadcut_amd._lib`` loads it. The measurement kernels of ``csrc/bench/``
-(not part of the decode ABI) link into ``libthreadcut_bench.so`` beside it.
+(not part of the decode ABI) link into ``libthreadcut_bench.so`` beside it, and
+``libthreadcut_stamps.so`` is the whole library built with
+``-DTC_DECODE_STAMPS=1``: the decode partial kernel then records a per-wave
+timeline (measurement only, ``bench.py --only decode-timeline``).
 When the repository's ``tests/c_host/tc_host.c`` is present, it is built too
 (gcc, C99): a host program that drives the library through the C ABI alone.
 Run as ``python -m threadcut_amd.build``.
@@ -21,6 +24,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libthreadcut_hip.so")
 BENCH_LIB = os.path.join(HERE, "libthreadcut_bench.so")
+STAMPS_LIB = os.path.join(HERE, "libthreadcut_stamps.so")
 ARCH = "gfx950"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 C_HOST = os.path.join(os.path.dirname(HERE), "tests", "c_host", "tc_host.c")
@@ -40,11 +44,11 @@ def hipcc():
     return path
 
 
-def _compile(src, obj):
+def _compile(src, obj, defines=()):
     if src.endswith(".cpp"):  # host-only C++
         cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", "-c", src, "-o", obj]
     else:
-        cmd = [hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
+        cmd = [hipcc(), *COMMON_FLAGS, *defines, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass reports the device-only feature flag as unknown; drop that noise.
     noise = "'-packed-fp32-ops' is not a recognized feature"
@@ -68,14 +72,22 @@ def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     bench_sources = sorted(glob.glob(os.path.join(CSRC, "bench", "*.hip")))
-    every = sources + bench_sources
-    objs = [os.path.join(BUILD, os.path.splitext(os.path.basename(s))[0] + ".o") for s in every]
+    os.makedirs(os.path.join(BUILD, "stamps"), exist_ok=True)
+    stamp_sources = [s for s in sources if s.endswith(".hip")]
+    every = sources + bench_sources + stamp_sources
+    objs = [os.path.join(BUILD, os.path.splitext(os.path.basename(s))[0] + ".o") for s in sources + bench_sources]
+    stamp_objs = [os.path.join(BUILD, "stamps", os.path.splitext(os.path.basename(s))[0] + ".o")
+                  for s in stamp_sources]
+    defines = [()] * (len(sources) + len(bench_sources)) + [("-DTC_DECODE_STAMPS=1",)] * len(stamp_sources)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(every))) as ex:
-        for src, warn in zip(every, ex.map(_compile, every, objs)):
+        for src, warn in zip(every, ex.map(_compile, every, objs + stamp_objs, defines)):
             if warn and verbose:
                 print(f"[{os.path.basename(src)}]\n{warn}", file=sys.stderr)
     _link(objs[:len(sources)], LIB)
     _link(objs[len(sources):], BENCH_LIB)
+    # The host-only objects are shared; only the HIP sources differ.
+    host_objs = [o for s, o in zip(sources, objs) if s.endswith(".cpp")]
+    _link(stamp_objs + host_objs, STAMPS_LIB)
     if os.path.exists(C_HOST):
         # The C host is a test program: a failure to build it is reported, and its tests then
         # fail, but the library stays usable.

@@ -72,6 +72,9 @@ namespace {
 #ifndef TC_DECODE_WPE_PAGED
 #define TC_DECODE_WPE_PAGED 2  // the same for the paged instantiations
 #endif
+#ifndef TC_DECODE_STAMPS
+#define TC_DECODE_STAMPS 0  // 1: the measurement build; every partial wave records a timeline
+#endif
 #ifndef TC_COMBINE_ROUND
 #define TC_COMBINE_ROUND 16  // splits per lane and round of the combine
 #endif
@@ -125,6 +128,13 @@ struct PartialArgs {
   // into the head slab of the pools.
   const int32_t* tok_off;
   int64_t tok_pitch;
+#if TC_DECODE_STAMPS
+  // Per wave ((b * heads + h) * splits + split) * waves + wave, 8 words:
+  // realtime-clock stamps (100 MHz) at the kernel's start, after the first
+  // tile's step, at the loop's end, after the merge barrier and after the
+  // partial stores are issued, then HW_REG_HW_ID and HW_REG_XCC_ID.
+  unsigned long long* stamps;
+#endif
 };
 
 struct CombineArgs {
@@ -282,10 +292,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
   __shared__ uint32_t s_vt[kWaves][kVStageWords];
-  __shared__ float s_acc[kWaves][8][kHeadDim];
-  __shared__ float s_m[kWaves][8];
-  __shared__ float s_l[kWaves][8];
+  // The merge's rows are padded by 16 words, so the float4 stores of the g
+  // heads (one head per 16 lanes) fall on distinct banks.
+  __shared__ float s_acc[kWaves][8][kHeadDim + 16];
+  __shared__ float s_m[8][kWaves];
+  __shared__ float s_l[8][kWaves];
 
+#if TC_DECODE_STAMPS
+  const unsigned long long st_start = __builtin_amdgcn_s_memrealtime();
+  unsigned long long st_first = 0, st_loop = 0, st_merge = 0;
+#endif
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;   // head column (also the token row of the K operand)
@@ -482,6 +498,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
       const int32_t tok1 = tok + tok_step, tok2 = tok1 + tok_step;
       load(t[1], tok1);
       step(t[0], tok, PAGED ? tok + t[0].rows : end);
+#if TC_DECODE_STAMPS
+      if (st_first == 0) st_first = __builtin_amdgcn_s_memrealtime();
+#endif
       load(t[0], tok2);
       if (tok1 < end) step(t[1], tok1, PAGED ? tok1 + t[1].rows : end);
       tok = tok2;
@@ -552,6 +571,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     }
   }
 
+#if TC_DECODE_STAMPS
+  st_loop = __builtin_amdgcn_s_memrealtime();
+  auto record = [&]() {
+    if (a.stamps && lane == 0) {
+      unsigned long long* o =
+          a.stamps + (((static_cast<int64_t>(b) * a.heads + h) * a.splits + split) * kWaves + wave) * 8;
+      o[0] = st_start; o[1] = st_first; o[2] = st_loop; o[3] = st_merge;
+      o[4] = __builtin_amdgcn_s_memrealtime();
+      o[5] = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);   // HW_REG_HW_ID
+      o[6] = __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20);  // HW_REG_XCC_ID
+    }
+  };
+#endif
   // The head's sum over the four lane groups; m is already common to them.
   l = rows_sum(l);
   const int64_t part = (static_cast<int64_t>(b) * a.heads + h) * a.splits + split;
@@ -567,6 +599,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
             make_float4(acc[bm][0] * inv, acc[bm][1] * inv, acc[bm][2] * inv, acc[bm][3] * inv);
       if (g == 0) a.lse_part[part * a.group + n] = (l == 0.f) ? neg_inf() : (m + __builtin_amdgcn_logf(l)) * kLn2;
     }
+#if TC_DECODE_STAMPS
+    st_merge = st_loop;
+    record();
+#endif
     return;
   }
   if (n < a.group) {
@@ -574,9 +610,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     for (int bm = 0; bm < 8; ++bm)
       *reinterpret_cast<float4*>(&s_acc[wave][n][16 * bm + 4 * g]) =
           make_float4(acc[bm][0], acc[bm][1], acc[bm][2], acc[bm][3]);
-    if (g == 0) { s_m[wave][n] = m; s_l[wave][n] = l; }
+    if (g == 0) { s_m[n][wave] = m; s_l[n][wave] = l; }
   }
+  // The split's output rows, addressed before the barrier (the address
+  // arithmetic is then off the path from the barrier to the stores).
+  float* const o_out = a.o_part + part * a.group * kHeadDim;
+  float* const l_out = a.lse_part + part * a.group;
+  __asm__ volatile("" ::"s"(o_out), "s"(l_out));
   __syncthreads();
+#if TC_DECODE_STAMPS
+  st_merge = __builtin_amdgcn_s_memrealtime();
+#endif
 
   // Each thread merges two adjacent dims of one head (one pass for G <= 4).
   for (int idx = threadIdx.x; idx < a.group * (kHeadDim / 2); idx += kThreads) {
@@ -586,8 +630,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     float2 ow[kWaves];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      mw[w] = s_m[w][hh];
-      lw[w] = s_l[w][hh];
+      mw[w] = s_m[hh][w];
+      lw[w] = s_l[hh][w];
       ow[w] = *reinterpret_cast<const float2*>(&s_acc[w][hh][d]);
     }
     float Mx = neg_inf();
@@ -604,10 +648,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     }
     // L >= 1 whenever a token was seen (the maximum contributes exp2(0)).
     const float inv = L == 0.f ? 0.f : __builtin_amdgcn_rcpf(L);
-    *reinterpret_cast<float2*>(a.o_part + (part * a.group + hh) * kHeadDim + d) = make_float2(O0 * inv, O1 * inv);
-    if (d == 0)
-      a.lse_part[part * a.group + hh] = (L == 0.f) ? neg_inf() : (Mx + __builtin_amdgcn_logf(L)) * kLn2;
+    *reinterpret_cast<float2*>(o_out + hh * kHeadDim + d) = make_float2(O0 * inv, O1 * inv);
+    if (d == 0) l_out[hh] = (L == 0.f) ? neg_inf() : (Mx + __builtin_amdgcn_logf(L)) * kLn2;
   }
+#if TC_DECODE_STAMPS
+  record();
+#endif
 }
 
 // Combine: one wave per (query head, kv head, sequence), a 3-D grid. Lane
@@ -661,10 +707,10 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a)
 #pragma unroll
     for (int j = 0; j < kCombineRound; ++j) {
       const int32_t s0 = r0 + 2 * j;
-      // The whole offset goes in the per-lane operand, which the buffer range
-      // checks: splits past S read zero.
-      ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, o_lane + s0 * o_split, 0, 0);
-      ls[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, l_lane + s0 * G * 4, 0, 0));
+      // The buffer range check covers the scalar offset too (measured on
+      // gfx950), so splits past S read zero.
+      ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, o_lane, s0 * o_split, 0);
+      ls[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, l_lane, s0 * G * 4, 0));
     }
     // Every load of the round is in flight before the first is consumed.
     __builtin_amdgcn_sched_barrier(0);
@@ -717,6 +763,10 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a)
 // ---------------------------------------------------------------------------
 // Host-side validation and launch.
 // ---------------------------------------------------------------------------
+
+#if TC_DECODE_STAMPS
+unsigned long long* g_stamps = nullptr;  // the stamp buffer partial launches record into (null: none)
+#endif
 
 int check_strides(const char* what, const int64_t* st, int n) {
   if (!st) return fail(TC_ERR_INVALID_ARGUMENT, "%s strides are null", what);
@@ -919,6 +969,9 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.page_tokens = paged ? paged->page_tokens : 0;
   a.tok_off = paged ? paged->tok_off : nullptr;
   a.tok_pitch = paged ? paged->tok_pitch : 0;
+#if TC_DECODE_STAMPS
+  a.stamps = g_stamps;
+#endif
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, s)
@@ -1234,3 +1287,10 @@ int tc_decode_paged_append_attention_at(const void* q_dev, const int64_t q_strid
 }
 
 }  // extern "C"
+
+#if TC_DECODE_STAMPS
+// Measurement build only (libthreadcut_stamps.so): the device buffer that the
+// partial kernels launched from now on record their wave timelines into
+// (8 words per wave, see PartialArgs::stamps), or null for none.
+extern "C" void tc_decode_set_stamps(void* stamps_dev) { tc::g_stamps = static_cast<unsigned long long*>(stamps_dev); }
+#endif
