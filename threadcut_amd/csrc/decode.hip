@@ -24,9 +24,10 @@
 //     16 (bf16) or 22 (fp16) significant bits. P^T leaves the S^T registers as
 //     the B operand without moving between lanes (lane l holds tokens
 //     4g..4g+3 of head n in both layouts). V is loaded as 4 tokens x 8 dims
-//     per lane, transposed in registers (v_perm) and written to the wave's
-//     own LDS region as V^T rows, which the A operand reads back 8 bytes per
-//     lane.
+//     per lane and stored row-major to the wave's own LDS region (16-byte
+//     stores, rows padded to 288 bytes); the A operand V^T comes back through
+//     the transposing ds_read_b64_tr_b16, so V is never transposed in
+//     registers.
 // The matrix core sums over a wave's tokens, so a wave's accumulator is
 // complete; the four waves of a work-group are merged through LDS and the
 // work-group writes one (o, lse) partial per query head.
@@ -45,9 +46,6 @@ namespace {
 #ifndef TC_DECODE_WAVES
 #define TC_DECODE_WAVES 4   // waves per partial work-group
 #endif
-#ifndef TC_DECODE_DEPTH
-#define TC_DECODE_DEPTH 2   // 16-token tiles in flight per wave
-#endif
 #ifndef TC_DECODE_AUX
 #define TC_DECODE_AUX 2     // cache-policy bits of the K/V buffer loads (2: non-temporal stream)
 #endif
@@ -59,12 +57,6 @@ namespace {
 #endif
 #ifndef TC_DECODE_WGS_PER_CU
 #define TC_DECODE_WGS_PER_CU 1  // partial work-groups per compute unit the split heuristic aims at
-#endif
-#ifndef TC_DECODE_VT
-#define TC_DECODE_VT 1  // V staging: 0 transposed in registers (v_perm), 1 row-major + transposing LDS reads
-#endif
-#ifndef TC_DECODE_LOOP
-#define TC_DECODE_LOOP 1  // tile loop: 1 loads only the tiles a wave owns
 #endif
 #ifndef TC_DECODE_WPE
 #define TC_DECODE_WPE 1  // amdgpu_waves_per_eu floor of the partial kernel (2 caps a wave at 256 registers)
@@ -83,7 +75,6 @@ constexpr int kHeadDim = 128;
 constexpr int64_t kMaxTokens = int64_t(1) << 29;  // token positions stay 32-bit in the kernel
 constexpr int kWaves = TC_DECODE_WAVES;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kDepth = TC_DECODE_DEPTH;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
 constexpr int kSplitGranule = kWaves * kWaveIter > 64 ? kWaves * kWaveIter : 64;  // split length granule
 constexpr float kLog2e = 1.4426950408889634f;
@@ -269,19 +260,12 @@ template <> struct DecodeMma<TC_DTYPE_BF16> {
   }
 };
 
-// V^T row of dim d in a wave's LDS region, in 32-bit words: 16 tokens (8
-// words) per row plus 4 words every 8 rows. The transposing 8-byte stores
-// (8 dims apart per lane) and the 8-byte A-operand reads (16 consecutive
-// dims) then hit distinct banks in each half-wave.
-__host__ __device__ constexpr int vt_word(int d) { return 8 * d + 4 * (d >> 3); }
-constexpr int kVtWords = vt_word(kHeadDim);   // per wave
 // Row-major V tile in a wave's LDS region: 16 token rows of 256 bytes, each
 // padded to 288 so that the transposing reads (4 rows x 32 bytes per 16-lane
 // group, 16 rows per instruction) and the 16-byte row stores fall on distinct
 // banks.
 constexpr int kVRowBytes = 2 * kHeadDim + 32;
 constexpr int kVTileWords = 16 * kVRowBytes / 4;
-constexpr int kVStageWords = TC_DECODE_VT ? kVTileWords : kVtWords;
 typedef short lds_s4 __attribute__((ext_vector_type(4)));
 constexpr float kLazyMax = 8.f;               // log2 units the running maximum may lag
 
@@ -291,7 +275,7 @@ template <int DT, bool PAGED, bool APPEND>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED ? TC_DECODE_WPE_PAGED : TC_DECODE_WPE))) void decode_partial_kernel(const PartialArgs a) {
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
-  __shared__ uint32_t s_vt[kWaves][kVStageWords];
+  __shared__ uint32_t s_vt[kWaves][kVTileWords];
   // The merge's rows are padded by 16 words, so the float4 stores of the g
   // heads (one head per 16 lanes) fall on distinct banks.
   __shared__ float s_acc[kWaves][8][kHeadDim + 16];
@@ -401,9 +385,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
       load_tile(tl, kslab, vslab, row_k, row_v, t0, end, koff, voff);
     }
   };
-  Tile t[kDepth];
-#pragma unroll
-  for (int d = 0; d < kDepth - 1; ++d) load(t[d], tok + d * tok_step);
+  Tile t[2];
+  load(t[0], tok);
 
   // Q as the B operand: head n, dims 32 i + 8 g .. +8 (zero for n >= G).
   uint4 qb[4];
@@ -416,7 +399,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     }
   }
 
-  uint32_t* vt = s_vt[wave];
   mfma_f4 acc[8];
 #pragma unroll
   for (int bm = 0; bm < 8; ++bm) acc[bm] = mfma_f4{0.f, 0.f, 0.f, 0.f};
@@ -429,26 +411,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     mfma_f4 s1 = M::qk(tl.k[1], qb[1], mfma_f4{0.f, 0.f, 0.f, 0.f});
     s0 = M::qk(tl.k[2], qb[2], s0);
     s1 = M::qk(tl.k[3], qb[3], s1);
-    // V into LDS while the matrix core works.
-#if TC_DECODE_VT
-    // Row-major: lane (g, n) stores tokens 4g + j, dims 8n .. 8n + 7.
-    char* vrow = reinterpret_cast<char*>(vt);
+    // V into LDS, row-major, while the matrix core works: lane (g, n)
+    // stores tokens 4g + j, dims 8n .. 8n + 7.
+    char* vrow = reinterpret_cast<char*>(s_vt[wave]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(vrow + (4 * g + j) * kVRowBytes + 16 * n) = tl.v[j];
-#else
-    // V^T rows, transposed in registers.
-    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&tl.v[0]);
-    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&tl.v[1]);
-    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&tl.v[2]);
-    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&tl.v[3]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      const uint32_t x01 = __builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel);
-      const uint32_t x23 = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);
-      *reinterpret_cast<uint2*>(vt + vt_word(8 * n + e) + 2 * g) = make_uint2(x01, x23);
-    }
-#endif
     float x[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -475,22 +442,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     const uint2 phi = make_uint2(h01, h23), plo = make_uint2(r01, r23);
 #pragma unroll
     for (int bm = 0; bm < 8; ++bm) {
-#if TC_DECODE_VT
       // A operand V^T[16 bm + n][4g .. 4g + 3]: ds_read_b64_tr_b16 hands lane n
       // of a 16-lane group element (n % 4) of what lane 4 j + n / 4 addressed,
       // for j = 0..3; lane (g, n) addresses row 4g + n / 4, dims 16 bm + 4 (n % 4).
       const lds_s4 t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) lds_s4*)(vrow + (4 * g + (n >> 2)) * kVRowBytes + 32 * bm + 8 * (n & 3)));
       const uint2 av = __builtin_bit_cast(uint2, t4);
-#else
-      const uint2 av = *reinterpret_cast<const uint2*>(vt + vt_word(16 * bm + n) + 2 * g);
-#endif
       acc[bm] = M::pv(av, phi, acc[bm]);
       acc[bm] = M::pv(av, plo, acc[bm]);
     }
   };
 
-#if TC_DECODE_LOOP
   // Two tiles in flight: the next tile's loads are issued before the current
   // tile is consumed, and no load is issued past the wave's last tile.
   if (tok < end) {
@@ -507,23 +469,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
       if (tok >= end) break;
     }
   }
-#else
-  if (tok < end) {
-    for (;;) {
-      bool done = false;
-#pragma unroll
-      for (int d = 0; d < kDepth; ++d) {
-        if (!done) {
-          load(t[(d + kDepth - 1) % kDepth], tok + (kDepth - 1) * tok_step);
-          step(t[d], tok, PAGED ? tok + t[d].rows : end);
-          tok += tok_step;
-          done = tok >= end;
-        }
-      }
-      if (done) break;
-    }
-  }
-#endif
 
   if (APPEND && split == 0 && wave == 0) {
     // The appended token as a tile whose only row is token 0 (the buffer
