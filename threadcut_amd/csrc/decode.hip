@@ -93,6 +93,7 @@ struct PartialArgs {
   int64_t sv_b, sv_h, sv_t;
   int heads, group, splits, split_tokens;
   int interleave;      // 0: split s owns tokens [s*T, (s+1)*T); 1: 16-token tiles dealt round-robin
+  int longest_first;   // per-sequence lengths, batch <= 64: work-group row z serves the z-th longest sequence
   float scale_log2;    // softmax scale * log2(e)
   // Append (k_new != null): the cache holds n - 1 tokens and the new token's
   // K/V rows [B, H, D] are attended from k_new/v_new and written to row n - 1
@@ -295,7 +296,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
   // XCD h and its partials stay in that XCD's L2 for the combine.
   const int h = blockIdx.x;
   const int split = blockIdx.y;
-  const int b = blockIdx.z;
+  // With per-sequence lengths the work-groups of the z-th longest sequence
+  // take grid row z, so the longest sequences are dispatched first (ties by
+  // index): lane j ranks sequence j by length, and the ballot finds the lane
+  // of rank z.
+  int b = blockIdx.z;
+  int32_t len_b = 0;  // longest-first: sequence b's length, read with the others
+  if (!PAGED && a.longest_first) {
+    const int B = static_cast<int>(gridDim.z);
+    const int32_t mine = lane < B ? a.lens[lane] : 0;
+    int rank = 0;
+    for (int i = 0; i < B; ++i) {
+      const int32_t other = __builtin_amdgcn_readlane(mine, i);
+      rank += (other > mine || (other == mine && i < lane)) ? 1 : 0;
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < B && rank == static_cast<int>(blockIdx.z));
+    b = hit ? __builtin_ctzll(hit) : b;
+    len_b = __builtin_amdgcn_readlane(mine, b);
+  }
 
   // Paged: the pools' head slabs, pages added per tile; otherwise sequence b's slabs.
   const char* kslab = reinterpret_cast<const char*>(a.k + (PAGED ? 0 : b * a.sk_b) + h * a.sk_h);
@@ -340,7 +358,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
     else if (APPEND)
       last_tile = ntiles - 1;
   } else if (a.lens) {
-    len = min(max(a.lens[b], 0), len_cap);
+    len = min(max(a.longest_first ? len_b : a.lens[b], 0), len_cap);
   }
   const int32_t end = a.interleave ? len : min(tok + wave_tokens, len);
 
@@ -898,6 +916,9 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.splits = num_splits;
   a.split_tokens = split_tokens;
   a.interleave = interleave;
+  // Longest sequences first: only for per-sequence lengths of a contiguous
+  // cache, and up to 64 sequences (one lane each).
+  a.longest_first = (lens_dev && !paged && batch > 1 && batch <= 64) ? 1 : 0;
   a.k_new = app ? static_cast<const uint16_t*>(app->k_new) : nullptr;
   a.v_new = app ? static_cast<const uint16_t*>(app->v_new) : nullptr;
   a.skn_b = app ? app->kn_strides[0] : 0;
