@@ -168,6 +168,20 @@ def test_ragged_with_empty_and_full_rows(gpu):
     assert np.abs(got - ref).max() <= TOL
 
 
+@pytest.mark.parametrize("lens", [[300, 300, 300, 300, 300, 300], [0, 513, 0, 513, 64, 64, 700],
+                                  [700 - (i % 5) * 100 for i in range(64)], [5 * (i % 3) for i in range(33)]])
+def test_ragged_longest_first_covers_every_sequence(gpu, lens):
+    """With per-sequence lengths the partial serves the sequences longest first (grid row z takes
+    the z-th longest, ties by index): ties, empty rows and 64 sequences must still give every
+    sequence exactly its own splits."""
+    print(f"case: ragged longest-first B={len(lens)} lens={lens[:8]}...", flush=True)
+    q, k, v, _ = workloads.decode_inputs(15, batch=len(lens), n=700)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    got = run_decode(q, k, v, gpu, lens=lens_t)
+    ref = f64_ref(q, k, v, lens=lens_t)
+    assert np.abs(got - ref).max() <= TOL
+
+
 @pytest.mark.parametrize("batch", [1, 4])
 def test_long_context_131072(gpu, batch):
     """131072 tokens (seed 4): many splits and the LSE combine, vs fp32 SDPA on the CPU."""
