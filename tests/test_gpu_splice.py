@@ -81,7 +81,8 @@ def test_full_splice_36_layers(gpu):
                                Split(0, 1000, 4001), Split(0, 32, 4000), Split(2, 34, 33), Split(3, 103, 4001),
                                Split(0, 511, 4490), Split(50, 300, 4701), Split(1, 32, 4000), Split(0, 47, 4000),
                                Split(1, 49, 4000), Split(0, 500, 4000), Split(0, 500, 4001), Split(9, 609, 4392),
-                               Split(5, 52, 300), Split(0, 40, 290), Split(7, 8, 257), Split(3, 20, 1111)])
+                               Split(5, 52, 300), Split(0, 40, 290), Split(7, 8, 257), Split(3, 20, 1111),
+                               Split(0, 45, 4000), Split(2, 48, 1000)])
 def test_overlapping_and_edge_splits(gpu, s):
     n = 5001
     ks, vs = workloads.layer_caches(21, 3, n)

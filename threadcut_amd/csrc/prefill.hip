@@ -14,8 +14,9 @@
 //                   each 32-key half for query row l%32 (the other 16 sit in
 //                   lane l^32), so a row's max and sum need one lane swap;
 //   O^T += V^T . P^T with P^T fed straight from those registers (fp16/bf16)
-//                   and V^T from LDS (V is transposed while staged), so P
-//                   never moves between lanes.
+//                   and V^T read from the V rows in LDS with the
+//                   transposing read (ds_read_b64_tr_b16), so P never moves
+//                   between lanes.
 // The online softmax runs per query row in fp32, log2 domain, as
 // p = exp2(s * c - m) with c = |scale| * log2(e) (a negative scale flips the
 // sign bits of Q instead). The running maximum m moves only when a tile's
@@ -30,8 +31,9 @@
 // follows from n and the causal diagonal; with a boolean mask it is read
 // from a map that tc_prefill_mask_tiles builds in one pass over the mask,
 // once per mask.
-// Tiles are double-buffered: the next active tile's global loads are in
-// flight while the current one is multiplied.
+// Tiles are double-buffered and loaded straight into LDS (16-byte buffer
+// loads with the LDS bit, no registers, no LDS stores): the next active
+// tile's loads are in flight while the current one is multiplied.
 #include <algorithm>
 #include <cmath>
 
@@ -49,15 +51,7 @@ constexpr int kHeadDim = 128;
 constexpr int kGroups = TC_PREFILL_GROUPS;
 constexpr int kRows = 4 * 32 * kGroups;  // query rows per work-group (4 waves)
 constexpr int kKeys = 64;          // keys per tile
-constexpr int kKStride = 136;      // halfs per K row in LDS (256 B + 16 B pad)
-constexpr int kVStride = 68;       // halfs per V^T row in LDS (128 B + 8 B pad)
-// V^T row of dim d: d + 2*(d / 32). With the 68-half stride this keeps the
-// 8-byte V^T reads (32 consecutive dims) and the transposing 8-byte stores
-// (8 dims apart) free of LDS bank conflicts.
-constexpr int kVRows = kHeadDim + 2 * (kHeadDim / 32 - 1);
-__host__ __device__ constexpr int vt_row(int d) { return d + 2 * (d >> 5); }
-constexpr int kKTile = kKeys * kKStride;
-constexpr int kVTile = kVRows * kVStride;
+constexpr int kRowBytes = 2 * kHeadDim;  // a K or V row in LDS (unpadded)
 
 // TILE_CAUSAL: the tile's mask is exactly the end-aligned causal rule
 // (key <= n - q_len + token), so its elements are tested arithmetically.
@@ -72,7 +66,6 @@ enum : int { TILE_SKIP = 0, TILE_FULL = 1, TILE_MIXED = 2, TILE_CAUSAL = 3 };
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -140,75 +133,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t by
                                            0x00020000);
 }
 
-__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, int32_t off, int32_t soff = 0) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// Staged registers of one K/V tile: thread t holds K chunks (key c/16,
-// dims 8*(c%16)) for c = t + 256*i, and V rows 4*(t/16)+i, dims 8*(t%16).
-struct Stage {
-  uint4 k[4];
-  uint4 v[4];
-};
-
-// Rows past n read as zeros (buffer range check); they are never visible.
-__device__ __forceinline__ void load_stage(Stage& s, const char* kslab, const char* vslab, int64_t row_k,
-                                           int64_t row_v, int64_t key0, int64_t n) {
-  const int t = threadIdx.x;
-  const int64_t rows = n - key0 < kKeys ? n - key0 : kKeys;
-  const __amdgpu_buffer_rsrc_t rk = rsrc(kslab + key0 * row_k, rows * row_k);
-  const __amdgpu_buffer_rsrc_t rv = rsrc(vslab + key0 * row_v, rows * row_v);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = t + 256 * i;
-    s.k[i] = bload(rk, static_cast<int32_t>((c >> 4) * row_k + 16 * (c & 15)));
-    s.v[i] = bload(rv, static_cast<int32_t>((4 * (t >> 4) + i) * row_v + 16 * (t & 15)));
-  }
-}
-
-// Paged: the same chunks, each row found through the byte offsets of the
-// tile's 64 keys, which every wave holds one per lane (idx: lane l has key
-// key0 + l, or kNoRow past the end, which reads zeros).
-constexpr int32_t kNoRow = INT32_MIN;  // as an unsigned offset, 2^31: past every buffer range
-__device__ __forceinline__ void load_stage_paged(Stage& s, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                                 int32_t idx) {
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int kk = (lane >> 4) + 4 * (t >> 6) + 16 * i;     // key of K chunk t + 256 i
-    const int kv = 4 * ((lane >> 4) + 4 * (t >> 6)) + i;    // key of V row i
-    const int32_t ok = __builtin_amdgcn_ds_bpermute(4 * kk, idx);
-    const int32_t ov = __builtin_amdgcn_ds_bpermute(4 * kv, idx);
-    s.k[i] = bload(rk, ok + 16 * (t & 15));
-    s.v[i] = bload(rv, ov + 16 * (t & 15));
-  }
-}
-
-// K rows as they are; V transposed to V^T[dim][key] (4 keys x 8 dims per thread).
-__device__ __forceinline__ void store_stage(const Stage& s, uint16_t* lk, uint16_t* lv) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = t + 256 * i;
-    *reinterpret_cast<uint4*>(lk + (c >> 4) * kKStride + 8 * (c & 15)) = s.k[i];
-  }
-  const int kq = t >> 4, dc = t & 15;
-  const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&s.v[0]);
-  const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&s.v[1]);
-  const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&s.v[2]);
-  const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&s.v[3]);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    // Element e of rows 0/1 and of rows 2/3 into one word each (v_perm_b32:
-    // low halves 0x05040100, high halves 0x07060302).
-    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-    const uint32_t x01 = __builtin_amdgcn_perm(w1[e >> 1], w0[e >> 1], sel);
-    const uint32_t x23 = __builtin_amdgcn_perm(w3[e >> 1], w2[e >> 1], sel);
-    *reinterpret_cast<uint2*>(lv + vt_row(8 * dc + e) * kVStride + 4 * kq) = make_uint2(x01, x23);
-  }
-}
+// Paged: the offset of a key past n (as an unsigned offset, 2^31: past every
+// buffer range, so the row reads zeros).
+constexpr int32_t kNoRow = INT32_MIN;
 
 // x combined with its value in lane l ^ 32 (v_permlane32_swap leaves both
 // halves' values in its two results).
@@ -237,8 +164,15 @@ template <int DT, int G, bool PAGED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_WAVES, TC_PREFILL_WAVES))) void prefill_kernel(
     const PrefillArgs a) {
   constexpr int kTokens = kRows / G;   // query tokens per work-group
-  __shared__ uint16_t s_k[2][kKTile];
-  __shared__ uint16_t s_v[2][kVTile];
+  // Tile buffers: K and V rows of 256 B, unpadded (a 16-byte load into LDS
+  // writes 64 lanes x 16 B in one run); chunk x of row r sits in slot
+  // x ^ sw(r), sw(r) = 4 (r % 4) + (r / 4) % 4, which spreads the K reads
+  // (16 rows, one chunk) and the transposing V reads (8 rows, 4 chunks)
+  // over all banks.
+  __shared__ __attribute__((aligned(1024))) uint16_t s_k0[kKeys * kHeadDim];
+  __shared__ __attribute__((aligned(1024))) uint16_t s_k1[kKeys * kHeadDim];
+  __shared__ __attribute__((aligned(1024))) uint16_t s_v0[kKeys * kHeadDim];
+  __shared__ __attribute__((aligned(1024))) uint16_t s_v1[kKeys * kHeadDim];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -310,50 +244,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     const bool apart = static_cast<uint32_t>(idx) != static_cast<uint32_t>(first) + lane * static_cast<uint32_t>(row_k);
     return (first >= 0 && __builtin_amdgcn_ballot_w64(apart) == 0) ? first : -1;
   };
-  // Load c of the eight of a stage (c < 4: K chunk t + 256 c; else V row c - 4), the
-  // chunks of load_stage / load_stage_paged. Paged: a row's offset is first +
-  // key * row for a contiguous tile (first >= 0), else taken from the lane of idx
-  // that holds it.
-  auto stage_part = [&](Stage& st_, int64_t tile, int32_t idx, int32_t first, int c) {
-    const int tt = threadIdx.x;
+  // Load c of the eight a thread issues per tile (c < 4: K, else V), straight
+  // into LDS: rows R = 16 wave + 4 (c % 4) + lane / 16, the lane filling slot
+  // lane % 16 of its row with chunk (lane % 16) ^ sw(R) = (lane % 16) ^
+  // (4 (lane / 16) + c % 4). Paged: a row's offset is first + key * row for a
+  // contiguous tile (first >= 0), else taken from the lane of idx that holds it.
+  const int dma_r = lane >> 4;
+  auto dma_part = [&](uint16_t* dk, uint16_t* dv, int64_t tile, int32_t idx, int32_t first, int c) {
     const int i = c & 3;
+    const int R = 16 * wave + 4 * i + dma_r;
+    const int x = (lane & 15) ^ (4 * dma_r + i);
+    __attribute__((address_space(3))) void* dst =
+        (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(c < 4 ? dk : dv) + (16 * wave + 4 * i) * kRowBytes);
     if constexpr (PAGED) {
-      const int ln = tt & 63;
-      const int kq = (ln >> 4) + 4 * (tt >> 6);  // K chunk t + 256 i: key kq + 16 i; V row i: key 4 kq + i
-      const int key = c < 4 ? kq + 16 * i : 4 * kq + i;
       if (first >= 0) {
-        // The lane's part of the offset in a register, the tile's and the chunk's in a scalar.
         const int32_t row = static_cast<int32_t>(row_k);
-        const int32_t lane_off = (c < 4 ? kq : 4 * kq) * row + 16 * (tt & 15);
-        const int32_t soff = first + (c < 4 ? 16 * i : i) * row;
-        if (c < 4)
-          st_.k[i] = bload(prk, lane_off, soff);
-        else
-          st_.v[i] = bload(prv, lane_off, soff);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c < 4 ? prk : prv, dst, 16, R * row + 16 * x, first, 0, 0);
       } else {
-        const int32_t off = __builtin_amdgcn_ds_bpermute(4 * key, idx) + 16 * (tt & 15);
-        if (c < 4)
-          st_.k[i] = bload(prk, off);
-        else
-          st_.v[i] = bload(prv, off);
+        const int32_t off = __builtin_amdgcn_ds_bpermute(4 * R, idx) + 16 * x;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c < 4 ? prk : prv, dst, 16, off, 0, 0, 0);
       }
     } else {
       const int64_t key0 = tile * kKeys;
       const int64_t rows = a.n - key0 < kKeys ? a.n - key0 : kKeys;
-      if (c < 4) {
-        const int cc = tt + 256 * i;
-        st_.k[i] = bload(rsrc(kslab + key0 * row_k, rows * row_k), static_cast<int32_t>((cc >> 4) * row_k + 16 * (cc & 15)));
-      } else {
-        st_.v[i] = bload(rsrc(vslab + key0 * row_v, rows * row_v),
-                         static_cast<int32_t>((4 * (tt >> 4) + i) * row_v + 16 * (tt & 15)));
-      }
+      if (c < 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(kslab + key0 * row_k, rows * row_k), dst, 16,
+                                                 static_cast<int32_t>(R * row_k + 16 * x), 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(vslab + key0 * row_v, rows * row_v), dst, 16,
+                                                 static_cast<int32_t>(R * row_v + 16 * x), 0, 0, 0);
     }
-  };
-  auto stage = [&](Stage& st_, int64_t tile, int32_t idx) {
-    if constexpr (PAGED)
-      load_stage_paged(st_, prk, prv, idx);
-    else
-      load_stage(st_, kslab, vslab, row_k, row_v, tile * kKeys, a.n);
   };
   const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.pitch : nullptr;
 
@@ -417,44 +337,66 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int v = 0; v < 16; ++v) o[rg][dt][v] = 0.f;
   }
 
+  // Byte offsets of the lane's K reads (chunk 2c + hi of row 32 kt + r32, kt
+  // adding 8 KB) and transposing V reads (rows 16p + 8rr + 4hi + j, chunk
+  // 4dt + 2(g&1) + q/2, byte 8(q&1) for lane 4j + q of 16-lane group g; p
+  // adding 4 KB).
+  int kaddr[8], vaddr[2][4];
+  {
+    const int swk = ((r32 & 3) << 2) | ((r32 >> 2) & 3);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) kaddr[c] = r32 * kRowBytes + 16 * ((2 * c + hi) ^ swk);
+    const int j = (lane & 15) >> 2, q = lane & 3, e = 2 * ((lane >> 4) & 1) + (q >> 1);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        vaddr[rr][dt] = (8 * rr + 4 * hi + j) * kRowBytes + 16 * ((4 * dt + e) ^ ((j << 2) | (2 * rr + hi))) + 8 * (q & 1);
+  }
+
   // Active tiles t (in LDS), tn (loading) and the class of each, found one
   // iteration ahead so the tile map's reads are off the critical path.
-  Stage st;
   int64_t t = next_active(t_begin);
   int cls_t = t < nt ? tile_class(t) : TILE_SKIP;
   if (t < nt) {
-    int32_t rows_t = kNoRow;
-    if constexpr (PAGED) rows_t = tile_rows(t);
-    stage(st, t, rows_t);
-    store_stage(st, s_k[0], s_v[0]);
+    int32_t rows_t = kNoRow, first_t = -1;
+    if constexpr (PAGED) {
+      rows_t = tile_rows(t);
+      first_t = contiguous_from(rows_t);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) dma_part(s_k0, s_v0, t, rows_t, first_t, c);
   }
   int64_t tn = t < nt ? next_active(t + 1) : nt;
   int cls_n = tn < nt ? tile_class(tn) : TILE_SKIP;
   // Paged: the row offsets of the tile loaded next, fetched one tile ahead.
   int32_t rows_n = kNoRow;
   if constexpr (PAGED) rows_n = tn < nt ? tile_rows(tn) : kNoRow;
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  int buf = 0;
-  while (t < nt) {
+  // One tile from (lk, lv) while the next one loads into (dk, dv).
+  auto body = [&](const uint16_t* lk, const uint16_t* lv, uint16_t* dk, uint16_t* dv) {
     const bool more = tn < nt;
-    const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, staged during this QK^T
+    const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, loaded during this QK^T
     int32_t first_tn = -1;
     if constexpr (PAGED) first_tn = more ? contiguous_from(rows_tn) : -1;
     const int64_t tnn = more ? next_active(tn + 1) : nt;
     const int cls_nn = tnn < nt ? tile_class(tnn) : TILE_SKIP;
     if constexpr (PAGED) rows_n = tnn < nt ? tile_rows(tnn) : kNoRow;
     const int cls = cls_t;
-    const uint16_t* lk = s_k[buf];
-    const uint16_t* lv = s_v[buf];
 
+    // The next tile's eight loads per thread go out first, in one burst: spread
+    // between the MFMAs below they stall the MFMA issue.
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dma_part(dk, dv, tn, rows_tn, first_tn, c);
+    }
     // S^T of the tile for every row group: each K fragment read from LDS
     // feeds kGroups MFMAs; the two 32-key halves are independent chains.
     // The K fragments are read four chunks ahead of their MFMAs; the
     // scheduling barriers keep the compiler from pulling the reads back next
-    // to their use (it otherwise waits out each read's latency). The next
-    // tile's eight global loads per thread go out one per chunk, between the
-    // MFMAs, instead of as one burst before them.
+    // to their use (it otherwise waits out each read's latency).
     float16v s[kGroups][2];
 #pragma unroll
     for (int rg = 0; rg < kGroups; ++rg)
@@ -464,7 +406,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
         for (int v = 0; v < 16; ++v) s[rg][kt][v] = 0.f;
     {
       auto kfrag = [&](int c, int kt) {
-        return *reinterpret_cast<const uint4*>(lk + (32 * kt + r32) * kKStride + 16 * c + 8 * hi);
+        return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(lk) + kaddr[c] + 32 * kRowBytes * kt);
       };
       uint4 kf[4][2];
 #pragma unroll
@@ -473,7 +415,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       for (int c = 0; c < 8; ++c) {
         const uint4 k0 = kf[c & 3][0], k1 = kf[c & 3][1];
         if (c + 4 < 8) { kf[c & 3][0] = kfrag(c + 4, 0); kf[c & 3][1] = kfrag(c + 4, 1); }
-        if (more) stage_part(st, tn, rows_tn, first_tn, c);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int rg = 0; rg < kGroups; ++rg) {
@@ -601,11 +542,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     // O^T += V^T . P^T: each V^T fragment read from LDS feeds kGroups MFMAs.
     // The four fragments of the next 16-key step are read one step ahead.
     {
+      typedef short vs4 __attribute__((ext_vector_type(4)));
       auto vfrag = [&](int p, int dt) {
-        const uint16_t* vp = lv + vt_row(32 * dt + r32) * kVStride + 32 * (p >> 1) + 16 * (p & 1) + 4 * hi;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-        const uint2 up = *reinterpret_cast<const uint2*>(vp + 8);
-        return make_uint4(lo.x, lo.y, up.x, up.y);
+        const char* vb = reinterpret_cast<const char*>(lv) + 16 * kRowBytes * p;
+        const vs4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) vs4*)(vb + vaddr[0][dt]));
+        const vs4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) vs4*)(vb + vaddr[1][dt]));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), u2 = __builtin_bit_cast(uint2, up);
+        return make_uint4(l2.x, l2.y, u2.x, u2.y);
       };
       uint4 vf[2][4];
 #pragma unroll
@@ -625,13 +568,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       }
     }
 
-    if (more) store_stage(st, s_k[buf ^ 1], s_v[buf ^ 1]);
+    // This thread's loads of tile tn have landed in LDS; then everyone's.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    buf ^= 1;
     t = tn;
     cls_t = cls_n;
     tn = tnn;
     cls_n = cls_nn;
+  };
+  while (t < nt) {
+    body(s_k0, s_v0, s_k1, s_v1);
+    if (t >= nt) break;
+    body(s_k1, s_v1, s_k0, s_v0);
   }
 
   // Normalize and write the lane's outputs: dims 32*dt + 8*j + 4*hi + 0..3 of each row.

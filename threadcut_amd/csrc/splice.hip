@@ -33,12 +33,15 @@ constexpr int kUnroll = TC_SPLICE_UNROLL;
 constexpr int kTileRows = kRowsPerPass * kUnroll;  // rows per work-group tile
 constexpr int kMaxJobs = 128;                      // strips sets per launch (64 layers x K,V)
 #ifndef TC_SPLICE_CHAIN_MIN
-#define TC_SPLICE_CHAIN_MIN 48
+#define TC_SPLICE_CHAIN_MIN 46
 #endif
 // An overlapping move (gap < rows moved) with a gap of at least this many rows
 // runs as gap independent chains per strip, one thread walking each
 // (splice_kernel with DEPTH > 0); shorter gaps walk each strip in row order
-// with one work-group. Chains win from about two work-groups per strip.
+// with one work-group. Chains win once the second work-group per strip has
+// most of its 32 chains: 36 layers x 12188 rows, gap 47 753-760 us chained
+// against 757-783 us walked, gap 44 757-779 either way, gaps 33-43 walked
+// 6-60 us faster.
 constexpr int64_t kChainMin = TC_SPLICE_CHAIN_MIN;
 // An overlapping move with a shorter gap walks each strip in row order, cut
 // into up to this many segments of at least kWalkMinRows rows that one
