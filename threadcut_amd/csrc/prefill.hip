@@ -540,7 +540,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     }
 
     // O^T += V^T . P^T: each V^T fragment read from LDS feeds kGroups MFMAs.
-    // The four fragments of the next 16-key step are read one step ahead.
+    // The four fragments of a 16-key step are read two steps ahead.
     {
       typedef short vs4 __attribute__((ext_vector_type(4)));
       auto vfrag = [&](int p, int dt) {
@@ -550,21 +550,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
         const uint2 l2 = __builtin_bit_cast(uint2, lo), u2 = __builtin_bit_cast(uint2, up);
         return make_uint4(l2.x, l2.y, u2.x, u2.y);
       };
-      uint4 vf[2][4];
+      uint4 vf[3][4];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) vf[0][dt] = vfrag(0, dt);
+      for (int p0 = 0; p0 < 2; ++p0)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) vf[p0][dt] = vfrag(p0, dt);
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
-        if (p < 3) {
+        if (p + 2 < 4) {
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) vf[(p + 1) & 1][dt] = vfrag(p + 1, dt);
+          for (int dt = 0; dt < 4; ++dt) vf[(p + 2) % 3][dt] = vfrag(p + 2, dt);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
           for (int rg = 0; rg < kGroups; ++rg)
-            o[rg][dt] = Mfma<DT>::mma(vf[p & 1][dt], pb[rg][p >> 1][p & 1], o[rg][dt]);
+            o[rg][dt] = Mfma<DT>::mma(vf[p % 3][dt], pb[rg][p >> 1][p & 1], o[rg][dt]);
       }
     }
 
