@@ -676,6 +676,96 @@ def measure_timeline(dev, n, steps):
     }
 
 
+def measure_prefill_timeline(dev, iters=20):
+    """Per-tile phase times of the prefill kernel on the engine chunk (2048 queries over 7716
+    cached tokens, bool causal mask): the measurement build libthreadcut_stamps.so has every
+    prefill wave record the shader clock at each tile's start, after its QK^T MFMAs are issued,
+    after the softmax, after its P.V MFMAs are issued and once the next tile's loads into LDS
+    have landed (the barrier follows). A tile's phases are: QK^T (the next tile's load burst
+    included), softmax, P.V, load wait and barrier (its end to the next tile's start).
+    Percentiles over every wave's tiles but its first two and last two, in shader-clock
+    cycles; the clock is the ratio of the shader clock to the 100 MHz realtime clock over each
+    wave's run."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from threadcut_amd import _lib, build, prefill, workloads
+
+    lib = ctypes.CDLL(build.STAMPS_LIB)
+    for name, (res, args) in _lib.SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    lib.tc_prefill_set_stamps.restype = None
+    lib.tc_prefill_set_stamps.argtypes = [ctypes.c_void_p]
+    L, n = workloads.PREFILL_CHUNK, workloads.PREFILL_PAST + workloads.PREFILL_CHUNK
+    q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, device=dev)
+    mask = workloads.causal_mask(L, n, device=dev)
+    g = HQ // HKV
+    splits = prefill.num_splits(1, L, n, HQ, HKV)
+    groups = -(-L * g // 128) * HKV * splits
+    words = 8 + 5 * 256
+    stamps = torch.zeros(groups * 4 * words, dtype=torch.int64, device=dev)
+
+    def timed(fn):
+        warm_eager(fn)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters * 1e3
+
+    saved = _lib._lib
+    _lib._lib = lib  # the prefill wrapper calls the measurement build from here on
+    try:
+        call = lambda: prefill.prefill_attention(q, k, v, mask, D ** -0.5, False)
+        call()
+        us_plain = timed(call)
+        lib.tc_prefill_set_stamps(ctypes.c_void_p(stamps.data_ptr()))
+        us_rec = timed(call)
+        stamps.zero_()
+        call()
+        torch.cuda.synchronize()
+    finally:
+        lib.tc_prefill_set_stamps(None)
+        _lib._lib = saved
+    raw = stamps.view(groups, 4, words).cpu().numpy().astype(np.int64)
+    head = raw[..., :8]
+    tiles = head[..., 5]
+    clock_ghz = np.median((head[..., 2] - head[..., 0]) / ((head[..., 3] - head[..., 1]) * 10.0))
+    phases = {"qk_with_load_burst": [], "softmax": [], "pv": [], "load_wait": [], "barrier": [], "tile": []}
+    for w in range(groups):
+        for wave in range(4):
+            nt = int(tiles[w, wave])
+            t = raw[w, wave, 8:8 + 5 * nt].reshape(nt, 5)
+            for i in range(2, nt - 2):
+                phases["qk_with_load_burst"].append(t[i, 1] - t[i, 0])
+                phases["softmax"].append(t[i, 2] - t[i, 1])
+                phases["pv"].append(t[i, 3] - t[i, 2])
+                phases["load_wait"].append(t[i, 4] - t[i, 3])
+                phases["barrier"].append(t[i + 1, 0] - t[i, 4])
+                phases["tile"].append(t[i + 1, 0] - t[i, 0])
+
+    def pct(x):
+        x = np.asarray(x, dtype=np.float64)
+        return {"p10": int(np.percentile(x, 10)), "median": int(np.median(x)), "p90": int(np.percentile(x, 90))}
+
+    span_us = (head[..., 3] - head[..., 1]).max(axis=1) / 100.0
+    return {
+        "workload": "prefill engine chunk: 2048 queries over 9764 keys (7716 cached), bool causal mask, fp16",
+        "work_groups": int(groups), "us_per_call": round(us_plain, 1), "us_per_call_recording": round(us_rec, 1),
+        "shader_clock_ghz_median": round(float(clock_ghz), 3),
+        "tile_phase_cycles": {k: pct(x) for k, x in phases.items()},
+        "tiles_per_work_group": {"min": int(tiles[:, 0].min()), "max": int(tiles[:, 0].max())},
+        "work_group_span_us": {"min": round(float(span_us.min()), 1), "median": round(float(np.median(span_us)), 1),
+                               "max": round(float(span_us.max()), 1)},
+    }
+
+
 def measure_decode_step(dev, n=10240, steps=40):
     """Whole-model decode step at the Qwen3-4B shape (random fp16 weights, 36 layers) at n
     cached tokens: the reference's eager per-token loop (engine.py:88-95) with the "threadcut"
@@ -985,7 +1075,7 @@ def main():
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
     ap.add_argument("--only", choices=["decode", "partial", "yardstick", "splice", "copy", "prefill", "decode-step",
-                                       "paged", "decode-timeline"],
+                                       "paged", "decode-timeline", "prefill-timeline"],
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -1020,6 +1110,9 @@ def main():
     if args.only == "decode-timeline":
         print(json.dumps({str(m): measure_timeline(dev, m, args.steps) for m in
                           ([args.n] if args.n != 10240 else [1536, 10240])}))
+        return
+    if args.only == "prefill-timeline":
+        print(json.dumps(measure_prefill_timeline(dev)))
         return
     if args.only == "decode-step":
         print(json.dumps(measure_decode_step(dev, args.n)))

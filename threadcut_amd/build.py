@@ -6,8 +6,10 @@ Compiles every ``csrc/*.hip`` source with hipcc (and the host-only
 ``threadcut_amd._lib`` loads it. The measurement kernels of ``csrc/bench/``
 (not part of the decode ABI) link into ``libthreadcut_bench.so`` beside it, and
 ``libthreadcut_stamps.so`` is the whole library built with
-``-DTC_DECODE_STAMPS=1``: the decode partial kernel then records a per-wave
-timeline (measurement only, ``bench.py --only decode-timeline``).
+``-DTC_DECODE_STAMPS=1 -DTC_PREFILL_STAMPS=1``: the decode partial kernel then
+records a per-wave timeline and the prefill kernel per-tile phase stamps
+(measurement only, ``bench.py --only decode-timeline`` and
+``--only prefill-timeline``).
 When the repository's ``tests/c_host/tc_host.c`` is present, it is built too
 (gcc, C99): a host program that drives the library through the C ABI alone.
 Run as ``python -m threadcut_amd.build``.
@@ -78,7 +80,7 @@ def build(verbose=False):
     objs = [os.path.join(BUILD, os.path.splitext(os.path.basename(s))[0] + ".o") for s in sources + bench_sources]
     stamp_objs = [os.path.join(BUILD, "stamps", os.path.splitext(os.path.basename(s))[0] + ".o")
                   for s in stamp_sources]
-    defines = [()] * (len(sources) + len(bench_sources)) + [("-DTC_DECODE_STAMPS=1",)] * len(stamp_sources)
+    defines = [()] * (len(sources) + len(bench_sources)) + [("-DTC_DECODE_STAMPS=1", "-DTC_PREFILL_STAMPS=1")] * len(stamp_sources)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(every))) as ex:
         for src, warn in zip(every, ex.map(_compile, every, objs + stamp_objs, defines)):
             if warn and verbose:

@@ -42,6 +42,9 @@
 namespace tc {
 namespace {
 
+#ifndef TC_PREFILL_STAMPS
+#define TC_PREFILL_STAMPS 0  // 1: the measurement build; every prefill wave records its tile phases
+#endif
 constexpr int kHeadDim = 128;
 // Row groups of 32 query rows per wave: each K/V fragment read from LDS
 // feeds that many MFMAs.
@@ -97,7 +100,18 @@ struct PrefillArgs {
   const int32_t* tok_off;
   int64_t tok_pitch;
   int64_t pool_bytes_k, pool_bytes_v;
+#if TC_PREFILL_STAMPS
+  // Per wave (work-group * 4 + wave), kStampWords words: a header of 8 (shader
+  // clock and realtime clock at the start, the same at the end, HW_REG_HW_ID
+  // | HW_REG_XCC_ID << 32, tiles recorded), then 5 shader-clock stamps per
+  // tile (its start, QK^T issued, softmax done, P.V issued, its loads landed).
+  unsigned long long* stamps;
+#endif
 };
+#if TC_PREFILL_STAMPS
+constexpr int kStampTiles = 256;
+constexpr int kStampWords = 8 + 5 * kStampTiles;
+#endif
 
 template <int DT> struct Mfma;
 template <> struct Mfma<TC_DTYPE_F16> {
@@ -178,6 +192,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hi = lane >> 5;            // which 16 keys of each 32-key half this lane holds
   const int r32 = lane & 31;           // the lane's query row within each 32-row group
+#if TC_PREFILL_STAMPS
+  unsigned long long* stw = a.stamps ? a.stamps + (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kStampWords : nullptr;
+  int st_tile = 0;
+  auto stamp = [&](int k) {
+    if (stw && st_tile < kStampTiles) {
+      const unsigned long long now = __builtin_amdgcn_s_memtime();
+      if (lane == 0) stw[8 + 5 * st_tile + k] = now;
+    }
+  };
+  if (stw && lane == 0) {
+    stw[0] = __builtin_amdgcn_s_memtime();
+    stw[1] = __builtin_amdgcn_s_memrealtime();
+    unsigned hw, xcc;
+    __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    stw[4] = hw | (static_cast<unsigned long long>(xcc) << 32);
+  }
+#else
+  auto stamp = [](int) {};
+#endif
 
   // Work item (KV head fastest, then key split, query block, batch):
   // consecutive work-groups go to different XCDs round-robin, so with
@@ -377,6 +411,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
   // One tile from (lk, lv) while the next one loads into (dk, dv).
   auto body = [&](const uint16_t* lk, const uint16_t* lv, uint16_t* dk, uint16_t* dv) {
+    stamp(0);
     const bool more = tn < nt;
     const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, loaded at this tile's start
     int32_t first_tn = -1;
@@ -424,6 +459,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       }
     }
 
+    stamp(1);
     uint4 pb[kGroups][2][2];
 #pragma unroll
     for (int rg = 0; rg < kGroups; ++rg) {
@@ -539,6 +575,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       l[rg] += lh[0] + lh[1];
     }
 
+    stamp(2);
     // O^T += V^T . P^T: each V^T fragment read from LDS feeds kGroups MFMAs.
     // The four fragments of a 16-key step are read two steps ahead.
     {
@@ -570,8 +607,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       }
     }
 
+    stamp(3);
     // This thread's loads of tile tn have landed in LDS; then everyone's.
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    stamp(4);
+#if TC_PREFILL_STAMPS
+    ++st_tile;
+#endif
     __syncthreads();
     t = tn;
     cls_t = cls_n;
@@ -584,6 +626,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     body(s_k1, s_v1, s_k0, s_v0);
   }
 
+#if TC_PREFILL_STAMPS
+  if (stw && lane == 0) {
+    stw[2] = __builtin_amdgcn_s_memtime();
+    stw[3] = __builtin_amdgcn_s_memrealtime();
+    stw[5] = static_cast<unsigned long long>(min(st_tile, kStampTiles));
+  }
+#endif
   // Normalize and write the lane's outputs: dims 32*dt + 8*j + 4*hi + 0..3 of each row.
 #pragma unroll
   for (int rg = 0; rg < kGroups; ++rg) {
@@ -683,8 +732,16 @@ __global__ __launch_bounds__(64) void mask_tiles_kernel(const uint8_t* mask, int
   }
 }
 
+#if TC_PREFILL_STAMPS
+unsigned long long* g_prefill_stamps = nullptr;  // the buffer prefill launches record into (null: none)
+#endif
+
 template <int DT, bool PAGED>
-void launch_attention(const PrefillArgs& a, int group, dim3 grid, hipStream_t stream) {
+void launch_attention(const PrefillArgs& a_in, int group, dim3 grid, hipStream_t stream) {
+  PrefillArgs a = a_in;
+#if TC_PREFILL_STAMPS
+  a.stamps = g_prefill_stamps;
+#endif
   switch (group) {
     case 1: hipLaunchKernelGGL((prefill_kernel<DT, 1, PAGED>), grid, dim3(256), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((prefill_kernel<DT, 2, PAGED>), grid, dim3(256), 0, stream, a); break;
@@ -999,3 +1056,12 @@ extern "C" int tc_prefill_paged_attention(const void* q_dev, const int64_t q_str
                       dtype, scale, num_splits, workspace_dev, workspace_bytes_in, out_dev, out_strides, stream,
                       &pools);
 }
+
+#if TC_PREFILL_STAMPS
+// Measurement build only (libthreadcut_stamps.so): the device buffer that the
+// prefill kernels launched from now on record their per-wave, per-tile phase
+// stamps into (kStampWords words per wave, see PrefillArgs::stamps), or null.
+extern "C" void tc_prefill_set_stamps(void* stamps_dev) {
+  tc::g_prefill_stamps = static_cast<unsigned long long*>(stamps_dev);
+}
+#endif
