@@ -413,7 +413,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   auto body = [&](const uint16_t* lk, const uint16_t* lv, uint16_t* dk, uint16_t* dv) {
     stamp(0);
     const bool more = tn < nt;
-    const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, loaded at this tile's start
+    const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, whose rows load at this tile's start
     int32_t first_tn = -1;
     if constexpr (PAGED) first_tn = more ? contiguous_from(rows_tn) : -1;
     const int64_t tnn = more ? next_active(tn + 1) : nt;
