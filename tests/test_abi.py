@@ -32,6 +32,15 @@ def test_every_declared_symbol_is_exported(lib):
         assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
 
 
+def test_measurement_build_exports_the_abi_and_its_stamp_setters():
+    """libthreadcut_stamps.so (the whole library built with the decode and prefill stamps)
+    exports every declared symbol plus the two setters bench.py's timelines call."""
+    from threadcut_amd import build
+    stamps = ctypes.CDLL(build.STAMPS_LIB)
+    for name in declared_symbols() + ["tc_decode_set_stamps", "tc_prefill_set_stamps"]:
+        assert hasattr(stamps, name), name
+
+
 def test_scratch_size_matches_header():
     m = re.search(r"#define TC_DECODE_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
     assert m and int(m.group(1)) << int(m.group(2)) == _lib.TC_DECODE_SCRATCH_BYTES
