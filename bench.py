@@ -755,6 +755,20 @@ def measure_prefill_timeline(dev, iters=20):
         return {"p10": int(np.percentile(x, 10)), "median": int(np.median(x)), "p90": int(np.percentile(x, 90))}
 
     span_us = (head[..., 3] - head[..., 1]).max(axis=1) / 100.0
+    # Work-groups i and i + groups/2 share a CU (the dispatcher's placement at two per CU): the
+    # tile times of the one with more tiles while its partner runs, and after the partner ended.
+    shared, alone = [], []
+    half = groups // 2
+    for w in range(half):
+        pair = (w, w + half)
+        long_w, short_w = (pair if tiles[pair[0], 0] >= tiles[pair[1], 0] else pair[::-1])
+        end_short = head[short_w, :, 2].max()
+        for wave in range(4):
+            nt = int(tiles[long_w, wave])
+            t = raw[long_w, wave, 8:8 + 5 * nt].reshape(nt, 5)[:, 0]
+            d = np.diff(t)
+            for i in range(2, nt - 2):
+                (alone if t[i] > end_short else shared).append(d[i])
     return {
         "workload": "prefill engine chunk: 2048 queries over 9764 keys (7716 cached), bool causal mask, fp16",
         "work_groups": int(groups), "us_per_call": round(us_plain, 1), "us_per_call_recording": round(us_rec, 1),
@@ -763,6 +777,8 @@ def measure_prefill_timeline(dev, iters=20):
         "tiles_per_work_group": {"min": int(tiles[:, 0].min()), "max": int(tiles[:, 0].max())},
         "work_group_span_us": {"min": round(float(span_us.min()), 1), "median": round(float(np.median(span_us)), 1),
                                "max": round(float(span_us.max()), 1)},
+        "longer_of_a_cu_pair_tile_cycles": {"partner_running": pct(shared) if shared else None,
+                                            "partner_done": pct(alone) if alone else None},
     }
 
 
