@@ -680,17 +680,32 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* o_par
   if (row >= rows) return;
   const int d0 = 4 * (threadIdx.x & 31);
   const float* lp = lse_part + static_cast<int64_t>(b) * splits * rows + row;
+  const float* opp = o_part + (static_cast<int64_t>(b) * splits * rows + row) * kHeadDim + d0;
+  // Every split's log-sum-exp and partial in one batch of loads (split s past
+  // the count reads the last split again and weighs nothing), then the merge
+  // in split order.
+  constexpr int kMax = 16;
+  float ls[kMax];
+  float4 x[kMax];
+#pragma unroll
+  for (int s = 0; s < kMax; ++s) {
+    const int si = s < splits ? s : splits - 1;
+    ls[s] = lp[si * rows];
+    x[s] = *reinterpret_cast<const float4*>(opp + si * rows * kHeadDim);
+  }
   float mx = neg_inf();
-  for (int s = 0; s < splits; ++s) mx = fmaxf(mx, lp[s * rows]);
+#pragma unroll
+  for (int s = 0; s < kMax; ++s) mx = s < splits ? fmaxf(mx, ls[s]) : mx;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   float wsum = 0.f;
   if (mx != neg_inf()) {
-    const float* opp = o_part + (static_cast<int64_t>(b) * splits * rows + row) * kHeadDim + d0;
-    for (int s = 0; s < splits; ++s) {
-      const float w = __builtin_amdgcn_exp2f(lp[s * rows] - mx);
-      const float4 x = *reinterpret_cast<const float4*>(opp + s * rows * kHeadDim);
-      acc.x += w * x.x; acc.y += w * x.y; acc.z += w * x.z; acc.w += w * x.w;
-      wsum += w;
+#pragma unroll
+    for (int s = 0; s < kMax; ++s) {
+      if (s < splits) {
+        const float w = __builtin_amdgcn_exp2f(ls[s] - mx);
+        acc.x += w * x[s].x; acc.y += w * x[s].y; acc.z += w * x[s].z; acc.w += w * x[s].w;
+        wsum += w;
+      }
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
@@ -803,6 +818,7 @@ void tile_geometry(int64_t q_len, int64_t n, int group, int64_t* nblk, int64_t* 
 }
 
 constexpr int kMaxPrefillSplits = 16;
+static_assert(kMaxPrefillSplits <= 16, "prefill_combine_kernel loads at most 16 splits");
 constexpr int kMinSplitTiles = 4;    // keys per split: at least 256
 
 // Key splits of a call: 1 when the query blocks alone give every CU two
