@@ -619,11 +619,7 @@ def measure_timeline(dev, n, steps):
 
     from threadcut_amd import _lib, build, flash_decode, workloads
 
-    lib = ctypes.CDLL(build.STAMPS_LIB)
-    for name, (res, args) in _lib.SIGNATURES.items():
-        fn = getattr(lib, name)
-        fn.restype = res
-        fn.argtypes = args
+    lib = _lib.bind(build.STAMPS_LIB)
     lib.tc_decode_set_stamps.restype = None
     lib.tc_decode_set_stamps.argtypes = [ctypes.c_void_p]
     qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
@@ -693,11 +689,7 @@ def measure_prefill_timeline(dev, iters=20):
 
     from threadcut_amd import _lib, build, prefill, workloads
 
-    lib = ctypes.CDLL(build.STAMPS_LIB)
-    for name, (res, args) in _lib.SIGNATURES.items():
-        fn = getattr(lib, name)
-        fn.restype = res
-        fn.argtypes = args
+    lib = _lib.bind(build.STAMPS_LIB)
     lib.tc_prefill_set_stamps.restype = None
     lib.tc_prefill_set_stamps.argtypes = [ctypes.c_void_p]
     L, n = workloads.PREFILL_CHUNK, workloads.PREFILL_PAST + workloads.PREFILL_CHUNK
@@ -719,20 +711,18 @@ def measure_prefill_timeline(dev, iters=20):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / iters * 1e3
 
-    saved = _lib._lib
-    _lib._lib = lib  # the prefill wrapper calls the measurement build from here on
-    try:
-        call = lambda: prefill.prefill_attention(q, k, v, mask, D ** -0.5, False)
-        call()
-        us_plain = timed(call)
-        lib.tc_prefill_set_stamps(ctypes.c_void_p(stamps.data_ptr()))
-        us_rec = timed(call)
-        stamps.zero_()
-        call()
-        torch.cuda.synchronize()
-    finally:
-        lib.tc_prefill_set_stamps(None)
-        _lib._lib = saved
+    with _lib.using(lib):  # the prefill wrapper calls the measurement build in this block
+        try:
+            call = lambda: prefill.prefill_attention(q, k, v, mask, D ** -0.5, False)
+            call()
+            us_plain = timed(call)
+            lib.tc_prefill_set_stamps(ctypes.c_void_p(stamps.data_ptr()))
+            us_rec = timed(call)
+            stamps.zero_()
+            call()
+            torch.cuda.synchronize()
+        finally:
+            lib.tc_prefill_set_stamps(None)
     raw = stamps.view(groups, 4, words).cpu().numpy().astype(np.int64)
     head = raw[..., :8]
     tiles = head[..., 5]

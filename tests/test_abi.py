@@ -36,9 +36,15 @@ def test_measurement_build_exports_the_abi_and_its_stamp_setters():
     """libthreadcut_stamps.so (the whole library built with the decode and prefill stamps)
     exports every declared symbol plus the two setters bench.py's timelines call."""
     from threadcut_amd import build
-    stamps = ctypes.CDLL(build.STAMPS_LIB)
+    stamps = _lib.bind(build.STAMPS_LIB)
     for name in declared_symbols() + ["tc_decode_set_stamps", "tc_prefill_set_stamps"]:
         assert hasattr(stamps, name), name
+    # The wrappers call it inside `using` only.
+    default = _lib.load()
+    with _lib.using(stamps):
+        assert _lib.load() is stamps
+        assert _lib.load().tc_abi_version() == default.tc_abi_version()
+    assert _lib.load() is default
 
 
 def test_scratch_size_matches_header():

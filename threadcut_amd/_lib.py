@@ -4,6 +4,7 @@ The library is built in-tree by ``threadcut_amd.build``. Loading it is the
 only way to reach the kernels: there is no fallback, and a missing library
 raises ``RuntimeError`` naming the build command.
 """
+import contextlib
 import ctypes
 import functools
 import os
@@ -106,6 +107,32 @@ def load():
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+def bind(path):
+    """Load another build of the library (the same ABI, e.g. ``libthreadcut_stamps.so``) with the
+    signatures set; it is not made the wrappers' library (see ``using``)."""
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+@contextlib.contextmanager
+def using(lib):
+    """Within the block the wrappers call `lib` (a library from ``bind``) instead of the
+    default build; the default comes back on exit. For measurement runs in one thread."""
+    global _lib
+    saved = load()
+    with _lock:
+        _lib = lib
+    try:
+        yield lib
+    finally:
+        with _lock:
+            _lib = saved
 
 
 def check(rc, what):
