@@ -230,6 +230,19 @@ def test_strided_cache_views_and_scales(gpu):
     check(q * 4, k, v, causal=True, scale=1.0, label="large scores")
 
 
+def test_token_major_layouts(gpu):
+    """K and/or V stored token-major ([B, N, H, D] seen as [B, H, N, D]: a 2 KB row pitch) and the
+    two with different pitches, so the kernel's K and V rows come from different strides."""
+    q, k, v = workloads.prefill_inputs(12, q_len=100, n=333, device=gpu)
+    kt = k.transpose(1, 2).contiguous().transpose(1, 2)
+    vt = v.transpose(1, 2).contiguous().transpose(1, 2)
+    assert kt.stride(2) == 8 * 128 and kt.stride(1) == 128
+    mask = workloads.causal_mask(100, 333).to(gpu)
+    check(q, kt, vt, mask=mask, label="token-major K and V")
+    check(q, k, vt, mask=mask, label="token-major V only")
+    check(q, kt, v, causal=False, label="token-major K only, no mask")
+
+
 def test_through_attention_interface(gpu, monkeypatch):
     """attention.attention() takes the kernel for both prefill masks the model produces: the
     reference's route (repeat_kv + SDPA, attention.py:43-46) raises if it is reached."""
