@@ -672,6 +672,47 @@ def measure_timeline(dev, n, steps):
     }
 
 
+def measure_prefill_sweep(dev, iters=10):
+    """The prefill kernel across chunk lengths and cached contexts (Qwen3-4B heads, fp16, a bool
+    causal chunk mask; past 0 is a causal prompt through is_causal), each call timed in steady
+    state beside the reference's GPU route (repeat_kv + SDPA with the same mask)."""
+    import torch
+
+    from threadcut_amd import attention, prefill, workloads
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        warm_eager(fn)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters * 1e3
+
+    rows = []
+    for q_len in (256, 512, 1024, 2048, 4096):
+        for past in (0, 2048, 8192, 16384):
+            n = past + q_len
+            q, k, v = workloads.prefill_inputs(q_len + past, q_len=q_len, n=n, device=dev)
+            causal = past == 0
+            mask = None if causal else workloads.causal_mask(q_len, n, device=dev)
+            scale = D ** -0.5
+            us = timed(lambda: prefill.prefill_attention(q, k, v, mask, scale, causal))
+            ref = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
+                q, attention.repeat_kv(k, HQ // HKV), attention.repeat_kv(v, HQ // HKV), attn_mask=mask,
+                scale=scale, is_causal=causal))
+            tflops = prefill_flops(q_len, n, True) / (us * 1e-6) / 1e12
+            rows.append({"q_len": q_len, "past": past, "splits": prefill.num_splits(1, q_len, n, HQ, HKV),
+                         "us_per_call": round(us, 1), "tflops": round(tflops, 1),
+                         "frac_of_mfma_peak": round(tflops / PEAK_MFMA_F16, 4),
+                         "reference_route_us": round(ref, 1), "speedup": round(ref / us, 2)})
+            del q, k, v, mask
+    return {"what": "prefill_attention, Qwen3-4B heads (32 q / 8 kv, D=128), fp16, batch 1", "rows": rows}
+
+
 def measure_prefill_timeline(dev, iters=20):
     """Per-tile phase times of the prefill kernel on the engine chunk (2048 queries over 7716
     cached tokens, bool causal mask): the measurement build libthreadcut_stamps.so has every
@@ -1081,7 +1122,7 @@ def main():
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
     ap.add_argument("--only", choices=["decode", "partial", "yardstick", "splice", "copy", "prefill", "decode-step",
-                                       "paged", "decode-timeline", "prefill-timeline"],
+                                       "paged", "decode-timeline", "prefill-timeline", "prefill-sweep"],
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -1116,6 +1157,9 @@ def main():
     if args.only == "decode-timeline":
         print(json.dumps({str(m): measure_timeline(dev, m, args.steps) for m in
                           ([args.n] if args.n != 10240 else [1536, 10240])}))
+        return
+    if args.only == "prefill-sweep":
+        print(json.dumps(measure_prefill_sweep(dev)))
         return
     if args.only == "prefill-timeline":
         print(json.dumps(measure_prefill_timeline(dev)))

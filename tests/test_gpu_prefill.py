@@ -155,6 +155,10 @@ def test_short_chunk_on_long_cache_uses_splits(gpu):
     # 10 query blocks x 8 heads, times the splits, still fit two work-groups per CU.
     assert 80 * s <= 2 * torch.cuda.get_device_properties(gpu).multi_processor_count
     assert prefill.num_splits(1, 2048, 9764, 32, 8) == 1
+    # A chunk of half its keys or more (a prompt) runs unsplit; a short chunk on a longer cache splits.
+    for q_len, n in ((256, 256), (512, 512), (1024, 1024), (1024, 2048)):
+        assert prefill.num_splits(1, q_len, n, 32, 8) == 1, (q_len, n)
+    assert prefill.num_splits(1, 512, 2560, 32, 8) > 1
     q, k, v = workloads.prefill_inputs(40, q_len=300, n=10000, device=gpu)
     check(q, k, v, mask=workloads.causal_mask(300, 10000).to(gpu), label="short chunk")
 
