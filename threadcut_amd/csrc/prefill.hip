@@ -309,6 +309,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
                                                  static_cast<int32_t>(R * row_v + 16 * x), 0, 0, 0);
     }
   };
+  // The eight loads of a tile. Paged, the test for a one-page tile is taken
+  // once for the burst (a test per load left the compiler branching and
+  // waiting between the loads).
+  auto dma_tile = [&](uint16_t* dk, uint16_t* dv, int64_t tile, int32_t idx, int32_t first) {
+    if (PAGED && first >= 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dma_part(dk, dv, tile, idx, first, c);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) dma_part(dk, dv, tile, idx, -1, c);
+    }
+  };
   const uint8_t* tcls = a.tiles ? a.tiles + (bm * a.nblk + blk) * a.pitch : nullptr;
 
   // Tiles this work-group may need: its split's share of all n keys, cut at
@@ -398,8 +410,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       rows_t = tile_rows(t);
       first_t = contiguous_from(rows_t);
     }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) dma_part(s_k0, s_v0, t, rows_t, first_t, c);
+    dma_tile(s_k0, s_v0, t, rows_t, first_t);
   }
   int64_t tn = t < nt ? next_active(t + 1) : nt;
   int cls_n = tn < nt ? tile_class(tn) : TILE_SKIP;
@@ -424,8 +435,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     // The next tile's eight loads per thread go out first, in one burst: spread
     // between the MFMAs below they stall the MFMA issue.
     if (more) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) dma_part(dk, dv, tn, rows_tn, first_tn, c);
+      dma_tile(dk, dv, tn, rows_tn, first_tn);
     }
     // S^T of the tile for every row group: each K fragment read from LDS
     // feeds kGroups MFMAs; the two 32-key halves are independent chains.
