@@ -329,27 +329,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const int64_t key_end = a.causal ? min(a.n, past + last_tok + 1) : a.n;
   const int64_t t_begin = split * a.split_tiles;
   const int64_t nt = min((key_end + kKeys - 1) / kKeys, t_begin + a.split_tiles);
-  // The tile map row, eight classes a word: the 64 words from t_begin on sit
+  // The tile map row, eight one-byte classes a word, repacked to two bits a
+  // class (tile 8w + j of word w at bits 2j): the 64 words from t_begin on sit
   // one per lane and are read back with v_readlane (no memory access in the
-  // loop); farther words are loaded.
+  // loop); farther words are loaded. One register instead of two.
   const int64_t wbase = t_begin >> 3;
-  uint32_t map_lo = 0, map_hi = 0;
-  if (tcls && (wbase + lane) * 8 < a.pitch) {
-    const uint64_t x = reinterpret_cast<const uint64_t*>(tcls)[wbase + lane];
-    map_lo = static_cast<uint32_t>(x);
-    map_hi = static_cast<uint32_t>(x >> 32);
-  }
-  auto map_word = [&](int64_t w) -> uint64_t {
+  auto map_load = [&](int64_t w) -> uint32_t {
+    const uint64_t x = reinterpret_cast<const uint64_t*>(tcls)[w];
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r |= static_cast<uint32_t>((x >> (8 * j)) & 3u) << (2 * j);
+    return r;
+  };
+  const uint32_t map_pk = tcls && (wbase + lane) * 8 < a.pitch ? map_load(wbase + lane) : 0u;
+  auto map_bits = [&](int64_t w) -> uint32_t {
     const int64_t i = w - wbase;
-    if (i < 64) {
-      const int ii = static_cast<int>(i);
-      return static_cast<uint64_t>(__builtin_amdgcn_readlane(map_lo, ii)) |
-             (static_cast<uint64_t>(__builtin_amdgcn_readlane(map_hi, ii)) << 32);
-    }
-    return reinterpret_cast<const uint64_t*>(tcls)[w];
+    if (i < 64) return __builtin_amdgcn_readlane(map_pk, static_cast<int>(i));
+    return map_load(w);
   };
   auto tile_class = [&](int64_t t) -> int {
-    if (tcls) return static_cast<int>((map_word(t >> 3) >> (8 * (t & 7))) & 0xff);
+    if (tcls) return static_cast<int>((map_bits(t >> 3) >> (2 * (t & 7))) & 3u);
     if (a.mask) return TILE_MIXED;
     const int64_t key0 = t * kKeys;
     if (key0 + kKeys > a.n) return TILE_MIXED;
@@ -364,8 +363,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       return t;
     }
     while (t < nt) {
-      const uint64_t w = map_word(t >> 3) >> (8 * (t & 7));
-      if (w) return min(nt, t + (__builtin_ctzll(w) >> 3));
+      const uint32_t w = map_bits(t >> 3) >> (2 * (t & 7));
+      if (w) return min(nt, t + (__builtin_ctz(w) >> 1));
       t = (t & ~int64_t(7)) + 8;
     }
     return nt;
