@@ -129,6 +129,23 @@ def test_combine_and_attention_validation(lib):
     assert rc == _lib.TC_ERR_WORKSPACE
 
 
+def test_prefill_validation_before_any_device_call(lib):
+    st = _lib.i64x3(1 << 24, 1 << 20, 128)
+
+    def prefill(q_len=16, n=64, hq=32, hkv=8, d=128, dt=0, q=4096, causal=1):
+        return lib.tc_prefill_attention(q, st, 8192, st, 12288, st, None, None, None, 0, causal, q_len, n, 1, hq, hkv,
+                                        d, dt, 0.088, 0, None, 0, 16384, st, None)
+
+    assert prefill(d=64) == _lib.TC_ERR_UNSUPPORTED
+    assert prefill(hq=24) == _lib.TC_ERR_UNSUPPORTED                   # group 3
+    assert prefill(q_len=65) == _lib.TC_ERR_INVALID_ARGUMENT           # more queries than keys
+    assert prefill(q=4100) == _lib.TC_ERR_ALIGNMENT
+    # Key positions are 32-bit in the kernel: 2^30 keys or more are refused.
+    assert prefill(n=1 << 30) == _lib.TC_ERR_UNSUPPORTED
+    assert b"2^30" in lib.tc_last_error()
+    assert prefill(q_len=0, n=1 << 30) == _lib.TC_OK                   # nothing to do
+
+
 def test_splice_validation(lib):
     ptrs = _lib.ptr_array([4096, 8192])
     st = _lib.i64x3(0, 1 << 20, 128)

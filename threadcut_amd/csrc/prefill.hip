@@ -90,6 +90,7 @@ struct PrefillArgs {
   float* lse_part;          // splits > 1: [b, splits, L, hq] log2-sum-exp of the split (-inf if empty)
   int kv_heads, causal, neg, splits;
   int mask_words;           // mask rows 4-byte aligned: a tile's mask bytes load as words
+  int whole;                // contiguous K/V: (n + 128) rows of each fit 31 bits (one buffer range a slab)
   int fold_cus;             // > 0: pair work items w and W-1-w on one CU (see the kernel), W <= 2 x this
   float c;                  // |scale| * log2(e)
   // Paged K/V (prefill_kernel<DT, G, true>): k and v are page pools whose head
@@ -231,12 +232,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   int64_t blk = rest % a.nblk;
   const int b = static_cast<int>(rest / a.nblk);
   if (a.causal) blk = a.nblk - 1 - blk;  // longest rows first
-  const int64_t tok0 = blk * kTokens;
-  const int64_t past = a.n - a.q_len;
+  // Key and query positions and tile indices fit 32 bits (the host keeps n
+  // below 2^30), so the loop's bookkeeping is 32-bit scalar arithmetic.
+  const int32_t n32 = static_cast<int32_t>(a.n), q_len32 = static_cast<int32_t>(a.q_len);
+  const int32_t tok0 = static_cast<int32_t>(blk) * kTokens;
+  const int32_t past = n32 - q_len32;
   const int64_t bm = a.sm_b ? b : 0;
 
   // The wave's kGroups row groups of 32 rows: row = (token, head of the group).
-  int64_t tok[kGroups];
+  int32_t tok[kGroups];
   int hq[kGroups];
   bool row_ok[kGroups];
   const uint8_t* mrow[kGroups];
@@ -246,7 +250,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     const int row = (wave * kGroups + rg) * 32 + r32;
     tok[rg] = tok0 + row / G;
     hq[rg] = h * G + row % G;
-    row_ok[rg] = tok[rg] < a.q_len;
+    row_ok[rg] = tok[rg] < q_len32;
     mrow[rg] = a.mask ? a.mask + bm * a.sm_b + (row_ok[rg] ? tok[rg] : 0) * a.sm_q : nullptr;
     const uint16_t* qp = a.q + b * a.sq_b + hq[rg] * a.sq_h + (row_ok[rg] ? tok[rg] : 0) * a.sq_t + 8 * hi;
     const uint32_t flip = a.neg ? 0x80008000u : 0u;
@@ -261,14 +265,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   const char* kslab = reinterpret_cast<const char*>(a.k + (PAGED ? 0 : b * a.sk_b) + h * a.sk_h);
   const char* vslab = reinterpret_cast<const char*>(a.v + (PAGED ? 0 : b * a.sv_b) + h * a.sv_h);
   const int64_t row_k = a.sk_t * 2, row_v = a.sv_t * 2;
-  // Paged: buffer ranges over the pools from this head's slab on, and the
-  // offsets of a tile's 64 keys, one per lane (kNoRow past n).
-  const __amdgpu_buffer_rsrc_t prk = rsrc(kslab, PAGED ? static_cast<int32_t>(a.pool_bytes_k - h * a.sk_h * 2) : 0);
-  const __amdgpu_buffer_rsrc_t prv = rsrc(vslab, PAGED ? static_cast<int32_t>(a.pool_bytes_v - h * a.sv_h * 2) : 0);
+  // Buffer ranges from this head's slab on: paged, over the pools (and the
+  // offsets of a tile's 64 keys, one per lane, kNoRow past n); contiguous
+  // with `whole`, over the n rows (the rows past n read zeros).
+  const __amdgpu_buffer_rsrc_t prk =
+      rsrc(kslab, PAGED ? a.pool_bytes_k - h * a.sk_h * 2 : (a.whole ? static_cast<int64_t>(n32) * row_k : 0));
+  const __amdgpu_buffer_rsrc_t prv =
+      rsrc(vslab, PAGED ? a.pool_bytes_v - h * a.sv_h * 2 : (a.whole ? static_cast<int64_t>(n32) * row_v : 0));
   const int32_t* toff = PAGED ? a.tok_off + b * a.tok_pitch : nullptr;
-  auto tile_rows = [&](int64_t tile) -> int32_t {
-    const int64_t key = tile * kKeys + lane;
-    return key < a.n ? toff[key] : kNoRow;
+  auto tile_rows = [&](int32_t tile) -> int32_t {
+    const int32_t key = tile * kKeys + lane;
+    return key < n32 ? toff[key] : kNoRow;
   };
   // Paged: when a tile's 64 keys are consecutive rows of one page (key k at
   // offset first + k * row), the offset of key 0, else -1 (also for a tile
@@ -283,8 +290,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
   // lane % 16 of its row with chunk (lane % 16) ^ sw(R) = (lane % 16) ^
   // (4 (lane / 16) + c % 4). Paged: a row's offset is first + key * row for a
   // contiguous tile (first >= 0), else taken from the lane of idx that holds it.
+  // Contiguous: the slab's range with the tile's first row in the load's
+  // scalar offset (first >= 0, `whole`), else a range over the tile's rows.
   const int dma_r = lane >> 4;
-  auto dma_part = [&](uint16_t* dk, uint16_t* dv, int64_t tile, int32_t idx, int32_t first, int c) {
+  auto dma_part = [&](uint16_t* dk, uint16_t* dv, int32_t tile, int32_t idx, int32_t first, int c) {
     const int i = c & 3;
     const int R = 16 * wave + 4 * i + dma_r;
     const int x = (lane & 15) ^ (4 * dma_r + i);
@@ -298,9 +307,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
         const int32_t off = __builtin_amdgcn_ds_bpermute(4 * R, idx) + 16 * x;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(c < 4 ? prk : prv, dst, 16, off, 0, 0, 0);
       }
+    } else if (first >= 0) {
+      const int32_t row = static_cast<int32_t>(c < 4 ? row_k : row_v);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c < 4 ? prk : prv, dst, 16, R * row + 16 * x, tile * kKeys * row, 0, 0);
     } else {
-      const int64_t key0 = tile * kKeys;
-      const int64_t rows = a.n - key0 < kKeys ? a.n - key0 : kKeys;
+      const int32_t key0 = tile * kKeys;
+      const int32_t rows = n32 - key0 < kKeys ? n32 - key0 : kKeys;
       if (c < 4)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc(kslab + key0 * row_k, rows * row_k), dst, 16,
                                                  static_cast<int32_t>(R * row_k + 16 * x), 0, 0, 0);
@@ -309,11 +321,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
                                                  static_cast<int32_t>(R * row_v + 16 * x), 0, 0, 0);
     }
   };
-  // The eight loads of a tile. Paged, the test for a one-page tile is taken
-  // once for the burst (a test per load left the compiler branching and
-  // waiting between the loads).
-  auto dma_tile = [&](uint16_t* dk, uint16_t* dv, int64_t tile, int32_t idx, int32_t first) {
-    if (PAGED && first >= 0) {
+  // The eight loads of a tile. The test for a one-page tile (paged) or a
+  // slab in one range (contiguous) is taken once for the burst (a test per
+  // load left the compiler branching and waiting between the loads).
+  auto dma_tile = [&](uint16_t* dk, uint16_t* dv, int32_t tile, int32_t idx, int32_t first) {
+    if (!PAGED) first = a.whole ? 0 : -1;
+    if (first >= 0) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) dma_part(dk, dv, tile, idx, first, c);
     } else {
@@ -325,16 +338,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
   // Tiles this work-group may need: its split's share of all n keys, cut at
   // its last query's position when causal.
-  const int64_t last_tok = min(tok0 + kTokens, a.q_len) - 1;
-  const int64_t key_end = a.causal ? min(a.n, past + last_tok + 1) : a.n;
-  const int64_t t_begin = split * a.split_tiles;
-  const int64_t nt = min((key_end + kKeys - 1) / kKeys, t_begin + a.split_tiles);
+  const int32_t last_tok = min(tok0 + kTokens, q_len32) - 1;
+  const int32_t key_end = a.causal ? min(n32, past + last_tok + 1) : n32;
+  const int32_t split_tiles = static_cast<int32_t>(a.split_tiles);
+  const int32_t t_begin = split * split_tiles;
+  const int32_t nt = min((key_end + kKeys - 1) / kKeys, t_begin + split_tiles);
   // The tile map row, eight one-byte classes a word, repacked to two bits a
   // class (tile 8w + j of word w at bits 2j): the 64 words from t_begin on sit
   // one per lane and are read back with v_readlane (no memory access in the
   // loop); farther words are loaded. One register instead of two.
-  const int64_t wbase = t_begin >> 3;
-  auto map_load = [&](int64_t w) -> uint32_t {
+  const int32_t wbase = t_begin >> 3;
+  auto map_load = [&](int32_t w) -> uint32_t {
     const uint64_t x = reinterpret_cast<const uint64_t*>(tcls)[w];
     uint32_t r = 0;
 #pragma unroll
@@ -342,22 +356,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     return r;
   };
   const uint32_t map_pk = tcls && (wbase + lane) * 8 < a.pitch ? map_load(wbase + lane) : 0u;
-  auto map_bits = [&](int64_t w) -> uint32_t {
-    const int64_t i = w - wbase;
-    if (i < 64) return __builtin_amdgcn_readlane(map_pk, static_cast<int>(i));
+  auto map_bits = [&](int32_t w) -> uint32_t {
+    const int32_t i = w - wbase;
+    if (i < 64) return __builtin_amdgcn_readlane(map_pk, i);
     return map_load(w);
   };
-  auto tile_class = [&](int64_t t) -> int {
+  auto tile_class = [&](int32_t t) -> int {
     if (tcls) return static_cast<int>((map_bits(t >> 3) >> (2 * (t & 7))) & 3u);
     if (a.mask) return TILE_MIXED;
-    const int64_t key0 = t * kKeys;
-    if (key0 + kKeys > a.n) return TILE_MIXED;
+    const int32_t key0 = t * kKeys;
+    if (key0 + kKeys > n32) return TILE_MIXED;
     if (a.causal && key0 + kKeys - 1 > past + tok0) return TILE_MIXED;
     return TILE_FULL;
   };
   // First active tile at or after t (nt if none). With a map, eight classes
   // are tested per word (rows are 8-aligned and padded with SKIP).
-  auto next_active = [&](int64_t t) -> int64_t {
+  auto next_active = [&](int32_t t) -> int32_t {
     if (!tcls) {
       while (t < nt && tile_class(t) == TILE_SKIP) ++t;
       return t;
@@ -365,7 +379,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     while (t < nt) {
       const uint32_t w = map_bits(t >> 3) >> (2 * (t & 7));
       if (w) return min(nt, t + (__builtin_ctz(w) >> 1));
-      t = (t & ~int64_t(7)) + 8;
+      t = (t & ~7) + 8;
     }
     return nt;
   };
@@ -401,7 +415,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
 
   // Active tiles t (in LDS), tn (loading) and the class of each, found one
   // iteration ahead so the tile map's reads are off the critical path.
-  int64_t t = next_active(t_begin);
+  int32_t t = next_active(t_begin);
   int cls_t = t < nt ? tile_class(t) : TILE_SKIP;
   if (t < nt) {
     int32_t rows_t = kNoRow, first_t = -1;
@@ -411,7 +425,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     }
     dma_tile(s_k0, s_v0, t, rows_t, first_t);
   }
-  int64_t tn = t < nt ? next_active(t + 1) : nt;
+  int32_t tn = t < nt ? next_active(t + 1) : nt;
   int cls_n = tn < nt ? tile_class(tn) : TILE_SKIP;
   // Paged: the row offsets of the tile loaded next, fetched one tile ahead.
   int32_t rows_n = kNoRow;
@@ -426,7 +440,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
     const int32_t rows_tn = rows_n;  // paged: the row offsets of tile tn, whose rows load at this tile's start
     int32_t first_tn = -1;
     if constexpr (PAGED) first_tn = more ? contiguous_from(rows_tn) : -1;
-    const int64_t tnn = more ? next_active(tn + 1) : nt;
+    const int32_t tnn = more ? next_active(tn + 1) : nt;
     const int cls_nn = tnn < nt ? tile_class(tnn) : TILE_SKIP;
     if constexpr (PAGED) rows_n = tnn < nt ? tile_rows(tnn) : kNoRow;
     const int cls = cls_t;
@@ -476,10 +490,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
       uint32_t vis = 0xffffffffu;
       float mx = neg_inf();
       if (cls != TILE_FULL) {
-        const int64_t key0 = t * kKeys;
-        int64_t lim64 = a.n - key0;
-        if (a.causal || cls == TILE_CAUSAL) lim64 = min(lim64, past + tok[rg] + 1 - key0);
-        const int lim = static_cast<int>(max<int64_t>(-1, min<int64_t>(lim64, kKeys)));
+        const int32_t key0 = t * kKeys;
+        int32_t lim = n32 - key0;
+        if (a.causal || cls == TILE_CAUSAL) lim = min(lim, past + tok[rg] + 1 - key0);
+        lim = max(-1, min(lim, kKeys));
         vis = 0;
         if (cls == TILE_MIXED && mrow[rg]) {
           // The row's 32 mask bytes of the tile, keys 32 kt + 8 q + 4 hi + j,
@@ -491,7 +505,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TC_PREFILL_
           // The key < lim test hides what lies past lim.
           const uint8_t* mt = mrow[rg] + key0;
           uint32_t mw[8];
-          if (a.mask_words && key0 + kKeys <= a.n) {
+          if (a.mask_words && key0 + kKeys <= n32) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) mw[q] = reinterpret_cast<const uint32_t*>(mt)[2 * q + hi];
           } else {
@@ -956,6 +970,9 @@ int prefill_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
     return fail(TC_ERR_INVALID_ARGUMENT, "q_len %lld must be in [0, n_tokens %lld]", (long long)q_len,
                 (long long)n_tokens);
   if (q_len == 0) return TC_OK;
+  // Key positions and tile indices are 32-bit in the kernel.
+  if (n_tokens >= (int64_t(1) << 30))
+    return fail(TC_ERR_UNSUPPORTED, "n_tokens %lld: the prefill kernels take fewer than 2^30 keys", (long long)n_tokens);
   if (!q_dev || !k_dev || !v_dev || !out_dev) return fail(TC_ERR_INVALID_ARGUMENT, "null tensor pointer");
   if (!aligned16(q_dev) || !aligned16(k_dev) || !aligned16(v_dev) || !aligned16(out_dev))
     return fail(TC_ERR_ALIGNMENT, "q/k/v/out base pointers must be 16-byte aligned");
@@ -1014,6 +1031,7 @@ int prefill_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
   a.sm_b = mask_dev ? mask_strides[0] : 0;
   a.sm_q = mask_dev ? mask_strides[1] : 0;
   a.mask_words = mask_dev && reinterpret_cast<uintptr_t>(mask_dev) % 4 == 0 && a.sm_b % 4 == 0 && a.sm_q % 4 == 0;
+  a.whole = !pools && (n_tokens + 2 * kKeys) * 2 * std::max(k_strides[2], v_strides[2]) < (int64_t(1) << 31);
   a.so_b = out_strides[0]; a.so_t = out_strides[1]; a.so_h = out_strides[2];
   a.q_len = q_len;
   a.n = n_tokens;
