@@ -529,8 +529,9 @@ def _stream(dev):
 
 
 def measure_prefill(dev, steps, only_case=None):
-    """Prefill attention at the Qwen3-4B shape (32 q / 8 kv heads, D=128, fp16): the
-    GQA-native kernel vs the reference's GPU route (repeat_kv + SDPA with the same mask)."""
+    """Prefill attention at the Qwen3-4B shape (32 q / 8 kv heads, D=128, fp16, the reference
+    engine's dtype; the engine chunk also in bf16, the checkpoint's): the GQA-native kernel vs
+    the reference's GPU route (repeat_kv + SDPA with the same mask)."""
     import torch
 
     from threadcut_amd import attention, prefill, workloads
@@ -548,9 +549,11 @@ def measure_prefill(dev, steps, only_case=None):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / iters * 1e3
 
-    cases = [("chunk_2048_on_7716", workloads.PREFILL_CHUNK, workloads.PREFILL_PAST + workloads.PREFILL_CHUNK, True),
+    chunk_n = workloads.PREFILL_PAST + workloads.PREFILL_CHUNK
+    cases = [("chunk_2048_on_7716", workloads.PREFILL_CHUNK, chunk_n, True),
              ("chunk_300_on_9700", 300, 10000, True),
-             ("prompt_2048_causal", 2048, 2048, False)]
+             ("prompt_2048_causal", 2048, 2048, False),
+             ("chunk_2048_on_7716_bf16", workloads.PREFILL_CHUNK, chunk_n, True)]
     if only_case is not None:
         # One workload alone (for counter runs); "nomask_2048_on_9764" is the chunk shape without a mask.
         cases = [c for c in cases + [("nomask_2048_on_9764", 2048, 9764, None),
@@ -559,7 +562,8 @@ def measure_prefill(dev, steps, only_case=None):
             raise SystemExit(f"unknown prefill case {only_case}")
     out = {}
     for name, L, n, masked in cases:
-        q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, device=dev)
+        dtype = torch.bfloat16 if name.endswith("_bf16") else torch.float16
+        q, k, v = workloads.prefill_inputs(7, q_len=L, n=n, dtype=dtype, device=dev)
         mask = workloads.causal_mask(L, n, device=dev) if masked else None
         if masked == "holes":
             # Causal with one key in ten hidden at random: every active tile is
@@ -575,7 +579,7 @@ def measure_prefill(dev, steps, only_case=None):
             q, attention.repeat_kv(k, HQ // HKV), attention.repeat_kv(v, HQ // HKV), attn_mask=mask, scale=scale,
             is_causal=causal).transpose(1, 2).contiguous(), iters)
         tflops = prefill_flops(L, n, masked is not None) / (us * 1e-6) / 1e12
-        r = {"q_len": L, "kv_tokens": n,
+        r = {"q_len": L, "kv_tokens": n, "dtype": "bf16" if dtype == torch.bfloat16 else "f16",
              "mask": {True: "bool [1,1,q,n] causal", False: "is_causal", None: "none",
                       "holes": "bool [1,1,q,n] causal, 10% of keys hidden at random"}[masked],
              "splits": prefill.num_splits(1, L, n, HQ, HKV), "us_per_call": round(us, 1),
@@ -1128,7 +1132,7 @@ def main():
                          "the calibration kernel of the HBM byte counters")
     ap.add_argument("--prefill-case", default=None,
                     help="with --only prefill: one workload (chunk_2048_on_7716, chunk_300_on_9700, "
-                         "prompt_2048_causal, nomask_2048_on_9764)")
+                         "prompt_2048_causal, chunk_2048_on_7716_bf16, nomask_2048_on_9764, holes_2048_on_9764)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
