@@ -804,6 +804,19 @@ def measure_prefill_timeline(dev, iters=20):
             d = np.diff(t)
             for i in range(2, nt - 2):
                 (alone if t[i] > end_short else shared).append(d[i])
+    # By XCD (HW_REG_XCC_ID; with 8 KV heads each XCD runs one head's work-groups): its shader clock
+    # and when its work-groups with the most tiles end, from the launch's first wave start.
+    t0 = head[..., 1].min()
+    end_us = (head[..., 3].max(axis=1) - t0) / 100.0
+    xcc = (head[:, 0, 4] >> 32) & 0xF
+    wg_clock = (head[..., 2] - head[..., 0]).max(axis=1) / ((head[..., 3] - head[..., 1]).max(axis=1) * 10.0)
+    longest = tiles[:, 0] >= tiles[:, 0].max() - 8
+    by_xcd = {}
+    for x in sorted(set(int(v) for v in xcc)):
+        m = xcc == x
+        by_xcd[str(x)] = {"clock_ghz": round(float(np.median(wg_clock[m])), 3),
+                          "longest_work_groups_end_us": {"median": round(float(np.median(end_us[m & longest])), 1),
+                                                         "max": round(float(end_us[m].max()), 1)}}
     return {
         "workload": "prefill engine chunk: 2048 queries over 9764 keys (7716 cached), bool causal mask, fp16",
         "work_groups": int(groups), "us_per_call": round(us_plain, 1), "us_per_call_recording": round(us_rec, 1),
@@ -814,6 +827,7 @@ def measure_prefill_timeline(dev, iters=20):
                                "max": round(float(span_us.max()), 1)},
         "longer_of_a_cu_pair_tile_cycles": {"partner_running": pct(shared) if shared else None,
                                             "partner_done": pct(alone) if alone else None},
+        "by_xcd": by_xcd,
     }
 
 
