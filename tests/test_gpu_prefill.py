@@ -247,6 +247,27 @@ def test_token_major_layouts(gpu):
     check(q, kt, v, causal=False, label="token-major K only, no mask")
 
 
+def test_row_pitch_past_one_buffer_range(gpu):
+    """K/V rows 10 MiB apart: n + 128 rows span more than 2^31 bytes, so the kernel cannot address a
+    head's keys through one buffer range and takes a range per tile instead (the other tests, with
+    ordinary pitches, take the one range). One KV head, g = 4, the chunk and the causal prompt."""
+    n, q_len, pitch = 100, 36, 5 << 20  # elements between rows: (100 + 128) * 2 * pitch > 2^31 bytes
+    assert (n + 128) * 2 * pitch >= 1 << 31
+    q, k0, v0 = workloads.prefill_inputs(14, q_len=q_len, n=n, q_heads=4, kv_heads=1, device=gpu)
+    rows = []
+    for src in (k0, v0):
+        store = torch.zeros((n - 1) * pitch + 128, dtype=src.dtype, device=gpu)
+        view = store.as_strided((1, 1, n, 128), (n * pitch, n * pitch, pitch, 1))
+        view.copy_(src)
+        rows.append(view)
+    k, v = rows
+    assert k.stride(2) == pitch
+    mask = workloads.causal_mask(q_len, n).to(gpu)
+    check(q, k, v, mask=mask, label="10 MiB row pitch, chunk")
+    qp, _, _ = workloads.prefill_inputs(15, q_len=n, n=n, q_heads=4, kv_heads=1, device=gpu)
+    check(qp, k, v, causal=True, label="10 MiB row pitch, causal prompt")
+
+
 def test_through_attention_interface(gpu, monkeypatch):
     """attention.attention() takes the kernel for both prefill masks the model produces: the
     reference's route (repeat_kv + SDPA, attention.py:43-46) raises if it is reached."""
