@@ -67,9 +67,6 @@ namespace {
 #ifndef TC_DECODE_STAMPS
 #define TC_DECODE_STAMPS 0  // 1: the measurement build; every partial wave records a timeline
 #endif
-#ifndef TC_COMBINE_ROUND
-#define TC_COMBINE_ROUND 16  // splits per lane and round of the combine
-#endif
 
 constexpr int kHeadDim = 128;
 constexpr int64_t kMaxTokens = int64_t(1) << 29;  // token positions stay 32-bit in the kernel
@@ -619,15 +616,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
 #endif
 }
 
-// Combine: one wave per (query head, kv head, sequence), a 3-D grid. Lane
-// (half, quad) takes dims 4 quad .. 4 quad + 3 of splits half, half + 2,
-// half + 4, ...: in rounds of kCombineRound splits per lane, every load of a
-// round issued before any is consumed (one memory round trip per round; one
-// round covers up to 2 * kCombineRound splits). Each round folds its splits
-// into a running (max, sum, weighted o) with one exponential per split; one
-// permlane32 swap merges the two halves.
-constexpr int kCombineRound = TC_COMBINE_ROUND;   // splits per lane and round
-
 // x of the lane pair (l, l ^ 16) or (l, l ^ 32): the lower row's value in lo,
 // the upper row's in hi, in both lanes.
 template <bool ROW32>
@@ -639,37 +627,79 @@ __device__ __forceinline__ void swap_pair(float x, float& lo, float& hi) {
   hi = __uint_as_float(r[1]);
 }
 
+// x of lanes l and l ^ K (K = 8: DPP row rotate by 8; 16, 32: permlane swaps),
+// the lower lane's value in lo, the upper lane's in hi, in both lanes.
+template <int K>
+__device__ __forceinline__ void lane_pair(float x, int lane, float& lo, float& hi) {
+  if constexpr (K == 8) {
+    const float o = __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(x), 0x128, 0xf, 0xf, false));  // row_ror:8
+    const bool upper = (lane & 8) != 0;
+    lo = upper ? o : x;
+    hi = upper ? x : o;
+  } else {
+    swap_pair<K == 32>(x, lo, hi);
+  }
+}
+// One merge step of the (max, sum, weighted o) states of lanes l and l ^ K,
+// lower lane first, so both lanes hold the same bits afterwards.
+template <int K>
+__device__ __forceinline__ void combine_merge(float& M, float& L, float4& O, int lane) {
+  float m0, m1, x0, x1;
+  lane_pair<K>(M, lane, m0, m1);
+  const float Mx = fmaxf(m0, m1);
+  const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
+  const float f0 = __builtin_amdgcn_exp2f((m0 - Ms) * kLog2e);
+  const float f1 = __builtin_amdgcn_exp2f((m1 - Ms) * kLog2e);
+  lane_pair<K>(L, lane, x0, x1); L = x0 * f0 + x1 * f1;
+  lane_pair<K>(O.x, lane, x0, x1); O.x = x0 * f0 + x1 * f1;
+  lane_pair<K>(O.y, lane, x0, x1); O.y = x0 * f0 + x1 * f1;
+  lane_pair<K>(O.z, lane, x0, x1); O.z = x0 * f0 + x1 * f1;
+  lane_pair<K>(O.w, lane, x0, x1); O.w = x0 * f0 + x1 * f1;
+  M = Mx;
+}
+
+// Combine: one wave per (sequence, KV head, query head, quarter of the dims),
+// grid (heads, batch, group * 4), the KV head fastest, so with 8 heads head
+// h's waves run on XCD h, where the partial kernel wrote its partials. Lane
+// (sg, chunk) takes dims 32 q + 4 chunk .. + 3 of splits sg, sg + 8, sg + 16,
+// ...: four splits a lane per round of 32, every load of a round issued before
+// the first is consumed (one memory round trip per round). Each round folds
+// its splits into a running (max, sum, weighted o) with one exponential per
+// split; the eight split groups are then merged across lanes (a DPP row
+// rotate, permlane16 and permlane32 swaps). Spreading a head's dims over four
+// waves keeps each wave's loads to 8 a round (the one-wave-per-head form
+// issued 32).
 template <int DT>
 __global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a) {
   using E = Elem<DT>;
+  constexpr int kPer = 4;  // splits a lane loads per round
   const int lane = threadIdx.x;
-  const int quad = lane & 31;
-  const int half = lane >> 5;
-  // Grid (heads, batch, group), the KV head fastest: with 8 heads, head h's
-  // work-groups run on XCD h, where the partial kernel wrote its partials.
+  const int chunk = lane & 7;
+  const int sg = lane >> 3;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int g = blockIdx.z;
+  const int g = blockIdx.z >> 2;
+  const int qtr = blockIdx.z & 3;
   const int G = a.group;
   const int S = a.splits;
   const int64_t bh = static_cast<int64_t>(b) * a.heads + h;
   // Buffer ranges over this (sequence, head)'s partials: loads past them read zero.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.o_part + bh * S * G * kHeadDim, S * G * kHeadDim * 4);
   const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse_part + bh * S * G, S * G * 4);
-  // Per-lane byte offsets (split `half` of a round); the round's split r0 + 2 j
+  // Per-lane byte offsets (split sg of a round); the round's split r0 + 8 j
   // adds a wave-uniform offset.
   const int32_t o_split = G * kHeadDim * 4;  // bytes between splits
-  const int32_t o_lane = half * o_split + (g * kHeadDim + 4 * quad) * 4;
-  const int32_t l_lane = (half * G + g) * 4;
+  const int32_t o_lane = sg * o_split + (g * kHeadDim + 32 * qtr + 4 * chunk) * 4;
+  const int32_t l_lane = (sg * G + g) * 4;
 
   float M = neg_inf(), L = 0.f;
   float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int r0 = 0; r0 < S; r0 += 2 * kCombineRound) {
-    u32x4 ov[kCombineRound];
-    float ls[kCombineRound];
+  for (int r0 = 0; r0 < S; r0 += 8 * kPer) {
+    u32x4 ov[kPer];
+    float ls[kPer];
 #pragma unroll
-    for (int j = 0; j < kCombineRound; ++j) {
-      const int32_t s0 = r0 + 2 * j;
+    for (int j = 0; j < kPer; ++j) {
+      const int32_t s0 = r0 + 8 * j;
       // The buffer range check covers the scalar offset too (measured on
       // gfx950), so splits past S read zero.
       ov[j] = __builtin_amdgcn_raw_buffer_load_b128(ro, o_lane, s0 * o_split, 0);
@@ -678,18 +708,18 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a)
     // Every load of the round is in flight before the first is consumed.
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < kCombineRound; ++j)
-      if (r0 + 2 * j + half >= S) ls[j] = neg_inf();  // past the last split (the load read zero)
+    for (int j = 0; j < kPer; ++j)
+      if (r0 + 8 * j + sg >= S) ls[j] = neg_inf();  // past the last split (the load read zero)
     float mr = ls[0];
 #pragma unroll
-    for (int j = 1; j < kCombineRound; ++j) mr = fmaxf(mr, ls[j]);
+    for (int j = 1; j < kPer; ++j) mr = fmaxf(mr, ls[j]);
     const float Mn = fmaxf(M, mr);
     const float Ms = (Mn == neg_inf()) ? 0.f : Mn;
     const float f = __builtin_amdgcn_exp2f((M - Ms) * kLog2e);  // 0 while nothing was seen
     L *= f;
     O.x *= f; O.y *= f; O.z *= f; O.w *= f;
 #pragma unroll
-    for (int j = 0; j < kCombineRound; ++j) {
+    for (int j = 0; j < kPer; ++j) {
       const float w = __builtin_amdgcn_exp2f((ls[j] - Ms) * kLog2e);
       L += w;
       O.x += w * __uint_as_float(ov[j].x);
@@ -699,26 +729,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const CombineArgs a)
     }
     M = Mn;
   }
-  // Merge the two halves (lanes l and l ^ 32).
-  float Mo, Mx;
-  swap_pair<true>(M, Mo, Mx);
-  Mx = fmaxf(Mo, Mx);
-  const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
-  const float f = __builtin_amdgcn_exp2f((M - Ms) * kLog2e);
-  float lo, hi;
-  swap_pair<true>(L * f, lo, hi);
-  const float Lt = lo + hi;
-  float4 Ot;
-  swap_pair<true>(O.x * f, lo, hi); Ot.x = lo + hi;
-  swap_pair<true>(O.y * f, lo, hi); Ot.y = lo + hi;
-  swap_pair<true>(O.z * f, lo, hi); Ot.z = lo + hi;
-  swap_pair<true>(O.w * f, lo, hi); Ot.w = lo + hi;
-  if (half == 0) {
+  // Merge the split groups: lanes l ^ 8, l ^ 16 and l ^ 32.
+  combine_merge<8>(M, L, O, lane);
+  combine_merge<16>(M, L, O, lane);
+  combine_merge<32>(M, L, O, lane);
+  if (sg == 0) {
     // An empty cache (no splits, or every split empty) gives zeros.
-    const float inv = (Mx == neg_inf()) ? 0.f : 1.f / Lt;
-    const uint32_t w0 = E::bits(Ot.x * inv) | (E::bits(Ot.y * inv) << 16);
-    const uint32_t w1 = E::bits(Ot.z * inv) | (E::bits(Ot.w * inv) << 16);
-    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 4 * quad;
+    const float inv = (M == neg_inf()) ? 0.f : 1.f / L;
+    const uint32_t w0 = E::bits(O.x * inv) | (E::bits(O.y * inv) << 16);
+    const uint32_t w1 = E::bits(O.z * inv) | (E::bits(O.w * inv) << 16);
+    uint16_t* dst = a.out + b * a.so_b + h * a.so_h + g * a.so_g + 32 * qtr + 4 * chunk;
     *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
   }
 }
@@ -993,8 +1013,10 @@ int tc_decode_combine(const float* o_part_dev, const float* lse_part_dev, int ba
   a.heads = kv_heads;
   a.group = group;
   a.splits = num_splits;
-  const dim3 grid(kv_heads, batch, group), block(64);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // One wave per (KV head, sequence, query head, quarter of the dims), the KV
+  // head fastest.
+  const dim3 grid(kv_heads, batch, group * 4), block(64);
   if (dtype == TC_DTYPE_F16)
     hipLaunchKernelGGL((decode_combine_kernel<TC_DTYPE_F16>), grid, block, 0, s, a);
   else
