@@ -310,17 +310,29 @@ def stream_read_lib():
     return lib
 
 
+def layer_plans(qs, ks, vs, outs, split=None):
+    """One DecodePlan per layer, all on one workspace: the layers of a decode step run one
+    after another, so each layer's partials are written over the previous layer's (as the
+    eager path's per-call workspace from torch's caching allocator also is)."""
+    from threadcut_amd import flash_decode
+
+    plans, ws = [], None
+    for q, k, v, o in zip(qs, ks, vs, outs):
+        plans.append(flash_decode.DecodePlan(q, k, v, D ** -0.5, o, split=split, workspace=ws))
+        ws = plans[-1].workspace
+    return plans
+
+
 def measure_sweep(dev, n, steps, warmup, split, only, min_warm_ms=0.0):
     """36 sequential decode calls at n tokens (own K/V per layer) as one HIP graph; the
     partial pass alone and the streaming-read yardstick as graphs over the same layers."""
     import torch
 
-    from threadcut_amd import _lib, flash_decode, workloads
+    from threadcut_amd import _lib, workloads
 
     qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
     outs = [torch.empty_like(q) for q in qs]
-    plans = [flash_decode.DecodePlan(q, k, v, D ** -0.5, o, split=split or None)
-             for q, k, v, o in zip(qs, ks, vs, outs)]
+    plans = layer_plans(qs, ks, vs, outs, split=split or None)
     S = plans[0].splits
 
     def step():
@@ -444,7 +456,7 @@ def measure_append(dev, n, steps):
     the fused append-and-attend launch."""
     import torch
 
-    from threadcut_amd import _lib, flash_decode
+    from threadcut_amd import _lib
 
     g = torch.Generator(device=dev)
     g.manual_seed(5)
@@ -455,8 +467,7 @@ def measure_append(dev, n, steps):
     vn = [torch.randn((1, HKV, 1, D), generator=g, device=dev).half() for _ in range(LAYERS)]
     qs = [torch.randn((1, HKV, HQ // HKV, D), generator=g, device=dev).half() for _ in range(LAYERS)]
     outs = [torch.empty_like(q) for q in qs]
-    plans = [flash_decode.DecodePlan(q, k[:, :, :n], v[:, :, :n], D ** -0.5, o)
-             for q, k, v, o in zip(qs, ks, vs, outs)]
+    plans = layer_plans(qs, [k[:, :, :n] for k in ks], [v[:, :, :n] for v in vs], outs)
     lib = _lib.load()
     ws = plans[0].workspace
     st = _lib.i64x3(*ks[0].stride()[:3])
@@ -621,14 +632,14 @@ def measure_timeline(dev, n, steps):
     import numpy as np
     import torch
 
-    from threadcut_amd import _lib, build, flash_decode, workloads
+    from threadcut_amd import _lib, build, workloads
 
     lib = _lib.bind(build.STAMPS_LIB)
     lib.tc_decode_set_stamps.restype = None
     lib.tc_decode_set_stamps.argtypes = [ctypes.c_void_p]
     qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
     outs = [torch.empty_like(q) for q in qs]
-    plans = [flash_decode.DecodePlan(q, k, v, D ** -0.5, o) for q, k, v, o in zip(qs, ks, vs, outs)]
+    plans = layer_plans(qs, ks, vs, outs)
     for p in plans:
         p.lib = lib
     S = plans[0].splits
@@ -979,9 +990,22 @@ def measure_paged(dev, n, steps, page_tokens=64):
         for layer in range(LAYERS):
             cache.decode(layer, qs[layer], D ** -0.5, out=outs[layer])
 
-    ms = time_graph(capture(step), steps, 5)
+    ms = time_graph(capture(step), steps, 5, WARM_MS)
+    # Beside it, the contiguous decode of the same keys (gathered into [1, Hkv, n, D]
+    # per layer), timed the same way in the same run.
+    gathered = [cache.gather(layer, 0) for layer in range(LAYERS)]
+    outs_c = [torch.empty_like(q) for q in qs]
+    plans = layer_plans(qs, [k[None] for k, _ in gathered], [v[None] for _, v in gathered], outs_c)
+
+    def step_contiguous():
+        for p in plans:
+            p.run()
+
+    ms_c = time_graph(capture(step_contiguous), steps, 5, WARM_MS)
     out[f"decode_{n}"] = {"us_per_call": round(ms * 1e3 / LAYERS, 3),
-                          "GB/s": round(LAYERS * decode_bytes(n) / (ms * 1e-3) / 1e9, 1)}
+                          "GB/s": round(LAYERS * decode_bytes(n) / (ms * 1e-3) / 1e9, 1),
+                          "contiguous_us_per_call": round(ms_c * 1e3 / LAYERS, 3)}
+    del plans, gathered, outs_c
 
     # One decode step with the new token's K/V: written into its reserved slot by
     # two torch row copies per layer and then attended, against the fused call.

@@ -111,6 +111,51 @@ def test_append_at_graph_replays_advance(gpu):
         assert np.abs(out.float().cpu().numpy() - want).max() <= TOL
 
 
+def test_layer_plans_sharing_a_workspace(gpu):
+    """Six layers' DecodePlans on one workspace, captured as one graph and replayed three times with
+    new queries between replays: every layer's output equals its own plan's on a private workspace,
+    bit for bit, and the float64 closed form within the bar; a too-small workspace is refused."""
+    g = torch.Generator(device=gpu)
+    g.manual_seed(4)
+    layers, n = 6, 1500
+    qs = [torch.empty((1, 8, 4, 128), device=gpu).half() for _ in range(layers)]
+    ks = [torch.randn((1, 8, n, 128), generator=g, device=gpu).half() for _ in range(layers)]
+    vs = [torch.randn((1, 8, n, 128), generator=g, device=gpu).half() for _ in range(layers)]
+    outs = [torch.empty_like(q) for q in qs]
+    own = [torch.empty_like(q) for q in qs]
+    shared = None
+    plans = []
+    for q, k, v, o in zip(qs, ks, vs, outs):
+        plans.append(flash_decode.DecodePlan(q, k, v, SCALE, o, workspace=shared))
+        shared = plans[-1].workspace
+    privates = [flash_decode.DecodePlan(q, k, v, SCALE, o) for q, k, v, o in zip(qs, ks, vs, own)]
+    assert all(p.workspace.data_ptr() == shared.data_ptr() for p in plans)
+    for q in qs:
+        q.normal_()
+    for p in plans:
+        p.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for p in plans:
+            p.run()
+    for r in range(3):
+        for q in qs:
+            q.copy_(torch.randn(q.shape, generator=g, device=gpu).half())
+        graph.replay()
+        torch.cuda.synchronize()
+        for p in privates:
+            p.run()
+        torch.cuda.synchronize()
+        print(f"case: shared workspace, replay {r}", flush=True)
+        for i in range(layers):
+            assert torch.equal(outs[i], own[i]), i
+            assert np.abs(outs[i].float().cpu().numpy() - ref64(qs[i], ks[i], vs[i], n)).max() <= TOL
+    small = torch.empty(plans[0].workspace_bytes - 16, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError):
+        flash_decode.DecodePlan(qs[0], ks[0], vs[0], SCALE, outs[0], workspace=small)
+
+
 @pytest.fixture(scope="module")
 def model(gpu):
     torch.manual_seed(0)

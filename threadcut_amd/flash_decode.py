@@ -236,9 +236,17 @@ class DecodePlan:
     Holds the ctypes arguments and a workspace, so ``run()`` is one library
     call with no allocation (usable inside HIP graph capture). The tensors
     must stay alive and keep their storage while the plan is used.
+
+    ``workspace`` (a uint8 device tensor of at least ``workspace_bytes``) lets
+    plans that run one after another on one stream, such as the layers of a
+    decode step, share one buffer: each call's partials are then written over
+    the previous call's, whose lines are still in the L2 cache, and the
+    combine reads them there (36 layers at 10240 tokens: 10.8 against 11.3 us
+    a call with a buffer per layer). Plans sharing a workspace must not run
+    concurrently.
     """
 
-    def __init__(self, q, k, v, scale, out, lens=None, split=None):
+    def __init__(self, q, k, v, scale, out, lens=None, split=None, workspace=None):
         _check_qkv(q, k, v, "DecodePlan")
         b, hkv, g, d = q.shape
         self.lib = _lib.load()
@@ -248,7 +256,15 @@ class DecodePlan:
             self.splits = num_splits(b, hkv, k.shape[2], split, ragged)
             self.split_tokens = split_tokens(b, hkv, k.shape[2], split, ragged)
             nbytes = self.lib.tc_decode_workspace_bytes(b, hkv, g, d, self.splits)
-            self.workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+            self.workspace_bytes = max(nbytes, 16)
+            if workspace is None:
+                self.workspace = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=q.device)
+            else:
+                if (workspace.dtype != torch.uint8 or workspace.device != q.device or not workspace.is_contiguous()
+                        or workspace.numel() < self.workspace_bytes):
+                    raise ValueError(f"DecodePlan: workspace must be a contiguous uint8 tensor on {q.device} "
+                                     f"of at least {self.workspace_bytes} bytes")
+                self.workspace = workspace
         self.tensors = (q, k, v, out, lens)
         self.args = (q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k, True), v.data_ptr(),
                      _strides3(v, True), lens.data_ptr() if lens is not None else None, k.shape[2],
