@@ -619,14 +619,15 @@ QWEN3_4B_CONFIG = dict(vocab_size=151936, hidden_size=2560, intermediate_size=97
                        rope_theta=1e6, tie_word_embeddings=True)
 
 
-def measure_timeline(dev, n, steps):
+def measure_timeline(dev, n, steps, paged=False):
     """Per-wave timeline of the decode partial kernel at n tokens (36 layers in one graph, as the
     headline): the measurement build libthreadcut_stamps.so has every partial wave record the
     realtime clock (100 MHz) at its start, after its first tile's step, at its loop's end,
     after the merge barrier and after its partial stores are issued. Times are microseconds
     from the first wave start of the same launch; percentiles over all waves of all layers.
     The gap is from a launch's last store issue to the next launch's first wave start: the
-    partial's drain, the combine launch and its work, and the next launch."""
+    partial's drain, the combine launch and its work, and the next launch. With `paged` the
+    layers are read through a PagedKV's tile table (64-token pages from a shuffled free list)."""
     import ctypes
 
     import numpy as np
@@ -637,19 +638,30 @@ def measure_timeline(dev, n, steps):
     lib = _lib.bind(build.STAMPS_LIB)
     lib.tc_decode_set_stamps.restype = None
     lib.tc_decode_set_stamps.argtypes = [ctypes.c_void_p]
-    qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
-    outs = [torch.empty_like(q) for q in qs]
-    plans = layer_plans(qs, ks, vs, outs)
-    for p in plans:
-        p.lib = lib
-    S = plans[0].splits
+    if paged:
+        cache = paged_cache(dev, n, 5)
+        gq = torch.Generator(device=dev)
+        gq.manual_seed(6)
+        qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
+        outs = [torch.empty_like(q) for q in qs]
+        runs = [lambda i=i: cache.decode(i, qs[i], D ** -0.5, out=outs[i]) for i in range(LAYERS)]
+        S = lib.tc_decode_num_splits(1, HKV, 16 * cache.device_table()[2], 0, 0)
+    else:
+        qs, ks, vs = workloads.sweep_layers(n, LAYERS, 2, device=dev)
+        outs = [torch.empty_like(q) for q in qs]
+        plans = layer_plans(qs, ks, vs, outs)
+        for p in plans:
+            p.lib = lib
+        runs = [p.run for p in plans]
+        S = plans[0].splits
     waves = 4
     stamps = torch.zeros(LAYERS, HKV * S * waves * 8, dtype=torch.int64, device=dev)
 
     def step(record):
-        for i, p in enumerate(plans):
-            lib.tc_decode_set_stamps(stamps[i].data_ptr() if record else None)
-            p.run()
+        with _lib.using(lib):
+            for i, run in enumerate(runs):
+                lib.tc_decode_set_stamps(stamps[i].data_ptr() if record else None)
+                run()
         lib.tc_decode_set_stamps(None)
 
     g_plain = capture(lambda: step(False))
@@ -673,7 +685,7 @@ def measure_timeline(dev, n, steps):
     last = t[..., 4].reshape(LAYERS, -1).max(axis=1)
     xcc = (raw[..., 6] & 15).astype(int)
     return {
-        "kv_tokens": n, "splits": S, "layers": LAYERS,
+        "kv_tokens": n, "splits": S, "layers": LAYERS, "cache": "paged" if paged else "contiguous",
         "us_per_call": round(ms_plain * 1e3 / LAYERS, 3),
         "us_per_call_recording": round(ms_rec * 1e3 / LAYERS, 3),
         "events_us_from_launch_start": {nm: pct(rel[..., k]) for k, nm in enumerate(names)},
@@ -956,31 +968,38 @@ def measure_torch_reads(dev, n, reps=50):
     return out
 
 
+def paged_cache(dev, tokens, seed, page_tokens=64):
+    """A 36-layer PagedKV holding `tokens` random fp16 K/V rows of sequence 0, its pages
+    handed out from a shuffled free list (neighbouring tiles sit on scattered pages)."""
+    import random
+
+    import torch
+
+    from threadcut_amd.paged import PagedKV
+
+    cache = PagedKV(LAYERS, HKV, -(-tokens // page_tokens) + 4, page_tokens, device=dev)
+    random.Random(seed).shuffle(cache.table.free)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    cache.append(0, [torch.randn((HKV, tokens, D), generator=g, device=dev).half() for _ in range(LAYERS)],
+                 [torch.randn((HKV, tokens, D), generator=g, device=dev).half() for _ in range(LAYERS)])
+    return cache
+
+
 def measure_paged(dev, n, steps, page_tokens=64):
     """The paged cache (threadcut_amd.paged): a 36-layer decode sweep at n tokens read
     through the tile table, and the prune of the splice workload (Split(2048, 8668, 5668)
     on 14336 tokens), whose device work is the kept keys' in-place rotation. Pages are
     handed out from a shuffled free list, so neighbouring tiles sit on scattered pages."""
-    import random
     import time
 
     import torch
 
     from threadcut_amd import _lib, kv, workloads
-    from threadcut_amd.paged import PagedKV, PageTable, _cut, tiles_of
-
-    def filled(tokens, seed):
-        pages = -(-tokens // page_tokens) + 4
-        cache = PagedKV(LAYERS, HKV, pages, page_tokens, device=dev)
-        random.Random(seed).shuffle(cache.table.free)
-        g = torch.Generator(device=dev)
-        g.manual_seed(seed)
-        cache.append(0, [torch.randn((HKV, tokens, D), generator=g, device=dev).half() for _ in range(LAYERS)],
-                     [torch.randn((HKV, tokens, D), generator=g, device=dev).half() for _ in range(LAYERS)])
-        return cache
+    from threadcut_amd.paged import PageTable, _cut, tiles_of
 
     out = {"page_tokens": page_tokens}
-    cache = filled(n, 5)
+    cache = paged_cache(dev, n, 5, page_tokens)
     gq = torch.Generator(device=dev)
     gq.manual_seed(6)
     qs = [torch.randn((1, HKV, HQ // HKV, D), generator=gq, device=dev).half() for _ in range(LAYERS)]
@@ -1047,7 +1066,7 @@ def measure_paged(dev, n, steps, page_tokens=64):
     torch.cuda.empty_cache()
 
     s = workloads.SPLICE_SPLIT
-    cache = filled(workloads.SPLICE_TOKENS, 7)
+    cache = paged_cache(dev, workloads.SPLICE_TOKENS, 7, page_tokens)
     suffix = _cut(cache.table.frags[0], s.c0, s.c0 + s.c)
     tiles = tiles_of(suffix, page_tokens)
     t = torch.zeros((len(tiles), 4), dtype=torch.int32)
@@ -1164,7 +1183,8 @@ def main():
     ap.add_argument("--no-reports", action="store_true",
                     help="skip the other lengths, the ragged batch and the 131072-token calls")
     ap.add_argument("--only", choices=["decode", "partial", "yardstick", "splice", "copy", "prefill", "decode-step",
-                                       "paged", "decode-timeline", "prefill-timeline", "prefill-sweep"],
+                                       "paged", "decode-timeline", "decode-timeline-paged", "prefill-timeline",
+                                       "prefill-sweep"],
                     default=None,
                     help="run one measurement only (for profiling); copy: a plain 256 MiB device copy, "
                          "the calibration kernel of the HBM byte counters")
@@ -1199,6 +1219,10 @@ def main():
     if args.only == "decode-timeline":
         print(json.dumps({str(m): measure_timeline(dev, m, args.steps) for m in
                           ([args.n] if args.n != 10240 else [1536, 10240])}))
+        return
+    if args.only == "decode-timeline-paged":
+        print(json.dumps({"contiguous": measure_timeline(dev, args.n, args.steps),
+                          "paged": measure_timeline(dev, args.n, args.steps, paged=True)}))
         return
     if args.only == "prefill-sweep":
         print(json.dumps(measure_prefill_sweep(dev)))
