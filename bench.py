@@ -654,7 +654,7 @@ def measure_timeline(dev, n, steps, paged=False):
             p.lib = lib
         runs = [p.run for p in plans]
         S = plans[0].splits
-    waves = 4
+    waves = 2 if (n <= _lib.TC_DECODE_SHORT_TOKENS and not paged) else 4  # partial work-group shape
     stamps = torch.zeros(LAYERS, HKV * S * waves * 8, dtype=torch.int64, device=dev)
 
     def step(record):

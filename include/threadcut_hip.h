@@ -45,6 +45,13 @@ enum { TC_DTYPE_F16 = 0, TC_DTYPE_BF16 = 1 };
 /* Largest number of KV splits one decode call may use. */
 #define TC_MAX_SPLITS 4096
 
+/* Decode of caches up to this many tokens with one length for the batch (no
+ * per-sequence lengths; not paged, no fused append) runs the partial pass in
+ * two-wave work-groups over the same split plan. The tile dealing of
+ * tc_decode_partial_interleaved follows the same rule: 16-token tile t goes to
+ * split (t / w) % num_splits, w = 2 for such a cache, else 4. */
+#define TC_DECODE_SHORT_TOKENS 2048
+
 /* ------------------------------------------------------------------------ */
 /* Library information                                                       */
 /* ------------------------------------------------------------------------ */

@@ -52,6 +52,11 @@ def test_scratch_size_matches_header():
     assert m and int(m.group(1)) << int(m.group(2)) == _lib.TC_DECODE_SCRATCH_BYTES
 
 
+def test_short_cache_bound_matches_header():
+    m = re.search(r"#define TC_DECODE_SHORT_TOKENS (\d+)", open(HEADER).read())
+    assert m and int(m.group(1)) == _lib.TC_DECODE_SHORT_TOKENS
+
+
 def test_noalloc_refuses_plans_beyond_its_scratch(lib):
     # 16 x 8 KV heads x 8 query heads at 64-token splits of 4096 tokens: 33 MB of partials.
     # Refused on the host (the split length is given, so no device is queried).

@@ -349,11 +349,12 @@ def test_gate_keeps_the_reference_path_for_other_calls(gpu, monkeypatch, dtype, 
     assert np.abs(out.float().cpu().numpy() - ref).max() <= (1e-5 if dtype == torch.float32 else TOL)
 
 
-@pytest.mark.parametrize("n,split", [(1000, 64), (10240, None)])
+@pytest.mark.parametrize("n,split", [(1000, 64), (1000, None), (2048, None), (2049, None), (10240, None)])
 def test_interleaved_partials_cover_round_robin_tiles(gpu, n, split):
     """tc_decode_partial_interleaved: split s's partial is the softmax over the 16-token tiles
-    s*4 + w + j*4S (w < 4) of its head, in float64 within 1e-4; partial + combine is bit-identical
-    to tc_decode_attention (the same kernels and plan)."""
+    s*W + w + j*W*S (w < W) of its head, W = 2 waves for a cache of at most TC_DECODE_SHORT_TOKENS
+    tokens and 4 above, in float64 within 1e-4; partial + combine is bit-identical to
+    tc_decode_attention (the same kernels and plan)."""
     q, k, v, _ = workloads.decode_inputs(43, n=n)
     hkv, g, d = 8, 4, 128
     qd = q.to(gpu).reshape(1, hkv, g, d)
@@ -378,8 +379,9 @@ def test_interleaved_partials_cover_round_robin_tiles(gpu, n, split):
     assert torch.equal(out, ref)
     qn, kn, vn = q.float().numpy().reshape(hkv, g, d).astype(np.float64), k[0].float().numpy(), v[0].float().numpy()
     tiles = np.arange(-(-n // 16))
+    W = 2 if n <= _lib.TC_DECODE_SHORT_TOKENS else 4
     for s in range(S):
-        mine = tiles[(tiles // 4) % S == s]
+        mine = tiles[(tiles // W) % S == s]
         toks = (mine[:, None] * 16 + np.arange(16)[None]).ravel()
         toks = toks[toks < n]
         if len(toks) == 0:

@@ -24,6 +24,7 @@ TC_ERR_HIP = 5
 TC_DTYPE_F16 = 0
 TC_DTYPE_BF16 = 1
 TC_MAX_SPLITS = 4096
+TC_DECODE_SHORT_TOKENS = 2048  # caches up to this long: two-wave partial work-groups
 TC_DECODE_SCRATCH_BYTES = 8 << 20  # static scratch of tc_decode_attention_noalloc, per GPU
 
 _DTYPES = {torch.float16: TC_DTYPE_F16, torch.bfloat16: TC_DTYPE_BF16}

@@ -72,8 +72,16 @@ constexpr int kHeadDim = 128;
 constexpr int64_t kMaxTokens = int64_t(1) << 29;  // token positions stay 32-bit in the kernel
 constexpr int kWaves = TC_DECODE_WAVES;
 constexpr int kThreads = 64 * kWaves;
+// Short caches (at most TC_DECODE_SHORT_TOKENS tokens, one length for the
+// batch): partial work-groups of two waves over the same splits. A wave then
+// has two tiles where it had one, and the merge of two waves costs less than
+// that of four (36 layers, Qwen3-4B heads, call us: 512 tokens 5.76 against
+// 5.87, 1024 5.89 against 6.02, 1536 6.05 against 6.25, 2048 6.50 against
+// 6.84; at 3072 and 4096 tokens two waves are slower).
+constexpr int kShortWaves = 2;
 constexpr int kWaveIter = 16;                        // tokens per wave iteration
 constexpr int kSplitGranule = kWaves * kWaveIter > 64 ? kWaves * kWaveIter : 64;  // split length granule
+static_assert(kSplitGranule % (kShortWaves * kWaveIter) == 0, "short plans split at the same granule");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -269,16 +277,17 @@ constexpr float kLazyMax = 8.f;               // log2 units the running maximum 
 
 // APPEND: the kernel attends (and writes) the new token of an append call
 // (a.k_new != null); the other instantiation carries none of that code.
-template <int DT, bool PAGED, bool APPEND>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED ? TC_DECODE_WPE_PAGED : TC_DECODE_WPE))) void decode_partial_kernel(const PartialArgs a) {
+template <int DT, bool PAGED, bool APPEND, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(PAGED ? TC_DECODE_WPE_PAGED : TC_DECODE_WPE))) void decode_partial_kernel(const PartialArgs a) {
   using M = DecodeMma<DT>;
   using E = Elem<DT>;
-  __shared__ uint32_t s_vt[kWaves][kVTileWords];
+  // W waves per work-group (kWaves, or kShortWaves for short caches).
+  __shared__ uint32_t s_vt[W][kVTileWords];
   // The merge's rows are padded by 16 words, so the float4 stores of the g
   // heads (one head per 16 lanes) fall on distinct banks.
-  __shared__ float s_acc[kWaves][8][kHeadDim + 16];
-  __shared__ float s_m[8][kWaves];
-  __shared__ float s_l[8][kWaves];
+  __shared__ float s_acc[W][8][kHeadDim + 16];
+  __shared__ float s_m[8][W];
+  __shared__ float s_l[8][W];
 
 #if TC_DECODE_STAMPS
   const unsigned long long st_start = __builtin_amdgcn_s_memrealtime();
@@ -322,10 +331,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
   // The wave's first tile and the distance between its tiles.
   int32_t tok, tok_step, wave_tokens = 0;
   if (a.interleave) {
-    tok = (split * kWaves + wave) * kWaveIter;
-    tok_step = a.splits * kWaves * kWaveIter;
+    tok = (split * W + wave) * kWaveIter;
+    tok_step = a.splits * W * kWaveIter;
   } else {
-    wave_tokens = a.split_tokens / kWaves;
+    wave_tokens = a.split_tokens / W;
     tok = split * a.split_tokens + wave * wave_tokens;
     tok_step = kWaveIter;
   }
@@ -536,7 +545,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
   auto record = [&]() {
     if (a.stamps && lane == 0) {
       unsigned long long* o =
-          a.stamps + (((static_cast<int64_t>(b) * a.heads + h) * a.splits + split) * kWaves + wave) * 8;
+          a.stamps + (((static_cast<int64_t>(b) * a.heads + h) * a.splits + split) * W + wave) * 8;
       o[0] = st_start; o[1] = st_first; o[2] = st_loop; o[3] = st_merge;
       o[4] = __builtin_amdgcn_s_memrealtime();
       o[5] = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);   // HW_REG_HW_ID
@@ -547,7 +556,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
   // The head's sum over the four lane groups; m is already common to them.
   l = rows_sum(l);
   const int64_t part = (static_cast<int64_t>(b) * a.heads + h) * a.splits + split;
-  if constexpr (kWaves == 1) {
+  if constexpr (W == 1) {
     // One wave: its accumulator is the split's; lane (g, n) holds dims
     // 16 bm + 4 g .. + 3 of head n.
     if (n < a.group) {
@@ -583,24 +592,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PAGED 
 #endif
 
   // Each thread merges two adjacent dims of one head (one pass for G <= 4).
-  for (int idx = threadIdx.x; idx < a.group * (kHeadDim / 2); idx += kThreads) {
+  for (int idx = threadIdx.x; idx < a.group * (kHeadDim / 2); idx += 64 * W) {
     const int hh = idx / (kHeadDim / 2);
     const int d = 2 * (idx % (kHeadDim / 2));
-    float mw[kWaves], lw[kWaves];
-    float2 ow[kWaves];
+    float mw[W], lw[W];
+    float2 ow[W];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       mw[w] = s_m[hh][w];
       lw[w] = s_l[hh][w];
       ow[w] = *reinterpret_cast<const float2*>(&s_acc[w][hh][d]);
     }
     float Mx = neg_inf();
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, mw[w]);
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, mw[w]);
     const float Ms = (Mx == neg_inf()) ? 0.f : Mx;
     float L = 0.f, O0 = 0.f, O1 = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float f = __builtin_amdgcn_exp2f(mw[w] - Ms);
       L += lw[w] * f;
       O0 += ow[w].x * f;
@@ -773,22 +782,36 @@ int check_common(int batch, int kv_heads, int group, int head_dim, int dtype) {
 inline dim3 partial_grid(const PartialArgs& a, int batch) { return dim3(a.heads, a.splits, batch); }
 
 template <int DT, bool PAGED>
-void launch_partial_paged(const PartialArgs& a, int batch, hipStream_t stream) {
-  if (a.k_new)
-    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, true>), partial_grid(a, batch), dim3(kThreads), 0,
+void launch_partial_paged(const PartialArgs& a, int batch, int waves, hipStream_t stream) {
+  if (a.k_new) {
+    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, true, kWaves>), partial_grid(a, batch), dim3(kThreads), 0,
                        stream, a);
-  else
-    hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, false>), partial_grid(a, batch), dim3(kThreads), 0,
-                       stream, a);
+    return;
+  }
+  if constexpr (!PAGED) {
+    if (waves == kShortWaves) {
+      hipLaunchKernelGGL((decode_partial_kernel<DT, false, false, kShortWaves>), partial_grid(a, batch),
+                         dim3(64 * kShortWaves), 0, stream, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((decode_partial_kernel<DT, PAGED, false, kWaves>), partial_grid(a, batch), dim3(kThreads), 0,
+                     stream, a);
 }
 
 template <int DT>
-hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream) {
+hipError_t launch_partial_dt(const PartialArgs& a, int batch, int waves, hipStream_t stream) {
   if (a.tile_tab)
-    launch_partial_paged<DT, true>(a, batch, stream);
+    launch_partial_paged<DT, true>(a, batch, waves, stream);
   else
-    launch_partial_paged<DT, false>(a, batch, stream);
+    launch_partial_paged<DT, false>(a, batch, waves, stream);
   return hipGetLastError();
+}
+
+// Waves per partial work-group: two for a short cache with one length for the
+// batch, read by the plain call with its tiles dealt round-robin; else four.
+inline int partial_waves(int64_t n_tokens, bool lens, bool paged, bool append, int interleave) {
+  return (interleave && !lens && !paged && !append && n_tokens <= TC_DECODE_SHORT_TOKENS) ? kShortWaves : kWaves;
 }
 
 // Split plan of a call: S splits of T tokens each (S * T >= n, T a multiple of
@@ -799,7 +822,9 @@ hipError_t launch_partial_dt(const PartialArgs& a, int batch, hipStream_t stream
 // wave-tiles and never more than TC_MAX_SPLITS. Ragged batches (per-sequence
 // lengths) aim at TC_DECODE_RAGGED_WGS_PER_CU per unit: short sequences leave
 // their work-groups light, and many small work-groups let the dispatcher
-// balance the rest.
+// balance the rest. The plan does not depend on the work-group shape: a short
+// cache read by two-wave work-groups keeps the four-wave plan's splits (its
+// waves then take two tiles each where four-wave ones took one).
 int split_plan(int batch, int kv_heads, int64_t max_tokens, int split_tokens, int ragged, int* S_out, int* T_out) {
   if (batch < 1 || kv_heads < 1 || max_tokens < 0)
     return fail(TC_ERR_INVALID_ARGUMENT, "split query with batch %d, kv_heads %d, max_tokens %lld", batch, kv_heads,
@@ -960,8 +985,9 @@ int partial_impl(const void* q_dev, const int64_t q_strides[3], const void* k_de
 #endif
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, s)
-                                             : launch_partial_dt<TC_DTYPE_BF16>(a, batch, s);
+  const int waves = partial_waves(n_tokens, lens_dev != nullptr, paged != nullptr, app != nullptr, interleave);
+  const hipError_t e = dtype == TC_DTYPE_F16 ? launch_partial_dt<TC_DTYPE_F16>(a, batch, waves, s)
+                                             : launch_partial_dt<TC_DTYPE_BF16>(a, batch, waves, s);
   return hip_status(e, "decode_partial launch");
 }
 

@@ -268,7 +268,7 @@ class DecodePlan:
         self.tensors = (q, k, v, out, lens)
         self.args = (q.data_ptr(), _strides3(q), k.data_ptr(), _strides3(k, True), v.data_ptr(),
                      _strides3(v, True), lens.data_ptr() if lens is not None else None, k.shape[2],
-                     b, hkv, g, d, _lib.dtype_code(q.dtype), float(scale), self.split_tokens,
+                     b, hkv, g, d, _lib.dtype_code(q.dtype), float(scale), int(split or 0),
                      self.workspace.data_ptr(), self.workspace.numel(), out.data_ptr(), _strides3(out))
         n = k.shape[2]
         parts = b * hkv * self.splits * g
