@@ -109,8 +109,9 @@ int tc_decode_partial(const void* q_dev, const int64_t q_strides[3],
 
 /* The partial pass of tc_decode_attention: the same kernel and outputs as
  * tc_decode_partial, but the S splits share each head's 16-token tiles
- * round-robin (split s takes the tiles of waves 4s..4s+3 in every round of
- * 4S tiles) instead of owning contiguous slices, so the loads in flight stay
+ * round-robin (split s takes the tiles of waves ws..ws+w-1 in every round of
+ * wS tiles; w = 4, or 2 for a cache of at most TC_DECODE_SHORT_TOKENS tokens
+ * without lens_dev) instead of owning contiguous slices, so the loads in flight stay
  * adjacent in HBM. A split's partial is the softmax over its own tiles, and
  * tc_decode_combine merges the S partials into the same output as with
  * contiguous slices. For callers that merge partials themselves (for example
